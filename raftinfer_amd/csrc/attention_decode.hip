@@ -1,0 +1,660 @@
+// Online decode attention for gfx950: KV append, zero-workspace single-block
+// decode, split-K partitions with an fp32 log-sum-exp merge, the decode plan
+// and workspace layout, and the batched ragged decode.
+//
+// Host semantics (validation order, messages, plan/layout arithmetic) follow
+// cpp/kernels/qwen35_online_attention.cu:27-196 and :1071-1328.  Device work is
+// this build's own: one workgroup per (KV head, partition) serves the four
+// query heads of the GQA group, so each K/V byte is read from HBM once.
+#include "decode_scan.hpp"
+#include "raftinfer_amd/qwen35_online_attention.hpp"
+
+#include <atomic>
+
+namespace raftinfer::kernels {
+namespace {
+
+using namespace raftinfer::amd;
+using Err = Qwen35PrimitiveError;
+
+constexpr std::size_t kMinimumContextBucketTokens = 512;
+constexpr Qwen35DecodeAttentionMode kDefaultOnlineDecodeMode = Qwen35DecodeAttentionMode::split_k_256;
+
+__device__ unsigned int g_capacity_errors = 0;
+
+bool multiplication_fits(std::size_t a, std::size_t b) noexcept {
+  return a == 0 || b <= std::numeric_limits<std::size_t>::max() / a;
+}
+
+std::size_t cache_element_bytes_of(Qwen35KvCacheDType dtype) noexcept {
+  switch (dtype) {
+  case Qwen35KvCacheDType::f32: return sizeof(float);
+  case Qwen35KvCacheDType::bf16: return sizeof(bf16_bits);
+  }
+  return 0;
+}
+
+bool layout_known(Qwen35KvCacheLayout layout) noexcept {
+  return layout == Qwen35KvCacheLayout::token_major || layout == Qwen35KvCacheLayout::head_major;
+}
+
+// cpp/kernels/qwen35_online_attention.cu:96-139
+bool online_decode_signature_supported(Qwen35AttentionShape shape, RaftInferDataType act,
+                                       Qwen35KvCacheDType cache_dtype,
+                                       Qwen35KvCacheLayout layout) noexcept {
+  if (shape.tokens != 1 || shape.query_heads != 16 || shape.kv_heads != 4 ||
+      shape.head_dim != 256 || shape.max_context_tokens == 0 ||
+      shape.past_tokens >= shape.max_context_tokens)
+    return false;
+  if (act != RAFTINFER_DTYPE_F32 && act != RAFTINFER_DTYPE_BF16) return false;
+  const std::size_t eb = cache_element_bytes_of(cache_dtype);
+  if (eb == 0 || !layout_known(layout)) return false;
+  const std::size_t kv_size = shape.kv_heads * shape.head_dim;
+  if (!multiplication_fits(shape.max_context_tokens, kv_size)) return false;
+  const std::size_t plane = shape.max_context_tokens * kv_size;
+  return multiplication_fits(2, plane) && multiplication_fits(2 * plane, eb);
+}
+
+// cpp/kernels/qwen35_online_attention.cu:141-145
+bool model_signature(Qwen35AttentionShape shape) noexcept {
+  return shape.tokens == 1 && shape.query_heads == 16 && shape.kv_heads == 4 &&
+         shape.head_dim == 256 && shape.max_context_tokens != 0;
+}
+
+std::size_t ceil_div(std::size_t n, std::size_t d, const char *message) {
+  require<Err>(d != 0, message);
+  return n / d + (n % d == 0 ? 0 : 1);
+}
+
+// cpp/kernels/qwen35_online_attention.cu:171-183
+std::size_t partition_tokens_for_mode(Qwen35DecodeAttentionMode mode) {
+  switch (mode) {
+  case Qwen35DecodeAttentionMode::split_k_256: return 256;
+  case Qwen35DecodeAttentionMode::split_k_512: return 512;
+  case Qwen35DecodeAttentionMode::single_block:
+  case Qwen35DecodeAttentionMode::auto_select: return 0;
+  }
+  require<Err>(false, "unsupported online decode attention mode");
+  return 0;
+}
+
+// cpp/kernels/qwen35_online_attention.cu:185-196
+std::size_t context_bucket_tokens(Qwen35AttentionShape shape, std::size_t context_tokens) {
+  std::size_t bucket = kMinimumContextBucketTokens;
+  while (bucket < context_tokens && bucket < shape.max_context_tokens) {
+    if (bucket > std::numeric_limits<std::size_t>::max() / 2) {
+      bucket = shape.max_context_tokens;
+      break;
+    }
+    bucket *= 2;
+  }
+  return bucket < shape.max_context_tokens ? bucket : shape.max_context_tokens;
+}
+
+int grid_dim(std::size_t value, const char *message) {
+  require<Err>(value <= static_cast<std::size_t>(std::numeric_limits<int>::max()), message);
+  return static_cast<int>(value);
+}
+
+// ------------------------------------------------------------- kernels
+
+__device__ __forceinline__ std::size_t read_position(const std::uint32_t *device_position,
+                                                     std::size_t host_position) {
+  return device_position == nullptr ? host_position : static_cast<std::size_t>(*device_position);
+}
+
+// Writes one token's K and V (4 x 256 each) at the position, RNE-cast to
+// the cache dtype.  Grid: 4 x 256.
+template <typename ActT, typename CacheT>
+__global__ __launch_bounds__(256) void append_decode_kernel(
+    const ActT *__restrict__ key, const ActT *__restrict__ value, CacheT *__restrict__ cache,
+    std::size_t max_ctx, std::size_t host_position, bool head_major,
+    const std::uint32_t *device_position) {
+  const std::size_t position = read_position(device_position, host_position);
+  if (position >= max_ctx) return;
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  const int kvh = e >> 8;
+  const int d = e & 255;
+  const std::size_t idx = cache_row(head_major, position, kvh, max_ctx) + d;
+  const std::size_t plane = max_ctx * kKvHeads * kHeadDim;
+  Elem<CacheT>::store(cache, idx, Elem<ActT>::load(key, e));
+  Elem<CacheT>::store(cache, plane + idx, Elem<ActT>::load(value, e));
+}
+
+// Zero-workspace single-block decode: one workgroup per group of NH query
+// heads scans the whole context and writes the gated output.  Exits when the
+// plan's split threshold is reached (mirrors the device-side early exit of
+// cpp/kernels/qwen35_online_attention.cu:427-430).
+template <typename ActT, typename CacheT, int NH, int WAVES, int U>
+__global__ __launch_bounds__(WAVES * 64) void decode_single_block_kernel(
+    const ActT *__restrict__ query, const ActT *__restrict__ gate, ActT *__restrict__ output,
+    const CacheT *__restrict__ cache, std::size_t max_ctx, std::size_t host_position,
+    bool head_major, const std::uint32_t *device_position, std::size_t threshold) {
+  __shared__ ScanShared<NH, WAVES> sh;
+  const std::size_t position = read_position(device_position, host_position);
+  if (position >= max_ctx) return;
+  const std::size_t ctx = position + 1;
+  if (threshold != 0 && ctx >= threshold) return;
+  const std::size_t first_head = static_cast<std::size_t>(blockIdx.x) * NH;
+  const std::size_t kv_head = first_head / kGroup;
+  const CacheT *k_plane = cache;
+  const CacheT *v_plane = cache + max_ctx * kKvHeads * kHeadDim;
+  scan_range<ActT, CacheT, NH, WAVES, U>(query, first_head, k_plane, v_plane, head_major, max_ctx,
+                                         kv_head, 0, ctx, sh);
+  __syncthreads();
+  for (int o = threadIdx.x; o < NH * kHeadDim; o += WAVES * 64) {
+    const int h = o / kHeadDim, d = o % kHeadDim;
+    float mm, l, a;
+    combine_waves(sh, h, d, mm, l, a);
+    const std::size_t out_idx = (first_head + h) * kHeadDim + d;
+    const float gv = Elem<ActT>::load(gate, out_idx);
+    Elem<ActT>::store(output, out_idx, (a / l) * sigmoid_gate(gv));
+  }
+}
+
+// Split-K partition: workgroup (head group, partition p) scans tokens
+// [p*P, min(ctx, (p+1)*P)) and writes fp32 (max, sum, value[256]) per query
+// head at index qh*max_partitions + p, the reference workspace bookkeeping
+// (cpp/kernels/qwen35_online_attention.cu:602-691).
+template <typename ActT, typename CacheT, int NH, int WAVES, int U>
+__global__ __launch_bounds__(WAVES * 64) void decode_partition_kernel(
+    const ActT *__restrict__ query, const CacheT *__restrict__ cache, float *__restrict__ pmax,
+    float *__restrict__ psum, float *__restrict__ pval, std::size_t max_ctx,
+    std::size_t host_position, bool head_major, std::size_t capacity,
+    std::size_t max_partitions, std::size_t partition_tokens, std::size_t threshold,
+    const std::uint32_t *device_position) {
+  __shared__ ScanShared<NH, WAVES> sh;
+  const std::size_t position = read_position(device_position, host_position);
+  if (position >= max_ctx) return;
+  const std::size_t ctx = position + 1;
+  if (ctx < threshold) return;
+  const std::size_t unit = blockIdx.x / capacity;
+  const std::size_t partition = blockIdx.x % capacity;
+  const std::size_t begin = partition * partition_tokens;
+  if (begin >= ctx) return;
+  const std::size_t end = ctx < begin + partition_tokens ? ctx : begin + partition_tokens;
+  const std::size_t first_head = unit * NH;
+  const std::size_t kv_head = first_head / kGroup;
+  const CacheT *k_plane = cache;
+  const CacheT *v_plane = cache + max_ctx * kKvHeads * kHeadDim;
+  scan_range<ActT, CacheT, NH, WAVES, U>(query, first_head, k_plane, v_plane, head_major, max_ctx,
+                                         kv_head, begin, end, sh);
+  __syncthreads();
+  for (int o = threadIdx.x; o < NH * kHeadDim; o += WAVES * 64) {
+    const int h = o / kHeadDim, d = o % kHeadDim;
+    float mm, l, a;
+    combine_waves(sh, h, d, mm, l, a);
+    const std::size_t idx = (first_head + h) * max_partitions + partition;
+    if (d == 0) {
+      pmax[idx] = mm * kLn2;
+      psum[idx] = l;
+    }
+    pval[idx * kHeadDim + d] = a;
+  }
+}
+
+// Log-sum-exp merge over the active partitions of one query head plus the
+// sigmoid gate (cpp/kernels/qwen35_online_attention.cu:693-756).  A device
+// position needing more partitions than the plan's capacity writes NaN and
+// counts a capacity error instead of trapping.
+template <typename ActT>
+__global__ __launch_bounds__(256) void decode_merge_kernel(
+    const ActT *__restrict__ gate, ActT *__restrict__ output, const float *__restrict__ pmax,
+    const float *__restrict__ psum, const float *__restrict__ pval, std::size_t max_ctx,
+    std::size_t host_position, std::size_t partition_tokens, std::size_t max_partitions,
+    std::size_t capacity, std::size_t threshold, const std::uint32_t *device_position) {
+  const std::size_t position = read_position(device_position, host_position);
+  if (position >= max_ctx) return;
+  const std::size_t ctx = position + 1;
+  if (ctx < threshold) return;
+  const std::size_t active = ctx / partition_tokens + (ctx % partition_tokens ? 1 : 0);
+  const std::size_t head = blockIdx.x;
+  const int d = threadIdx.x;
+  const std::size_t out_idx = head * kHeadDim + d;
+  if (active > capacity) {
+    if (head == 0 && d == 0) atomicAdd(&g_capacity_errors, 1u);
+    Elem<ActT>::store(output, out_idx, __builtin_nanf(""));
+    return;
+  }
+  const std::size_t first = head * max_partitions;
+  float mm = -INFINITY;
+  for (std::size_t p = 0; p < active; ++p) mm = fmaxf(mm, pmax[first + p]);
+  float l = 0.f, a = 0.f;
+  for (std::size_t p = 0; p < active; ++p) {
+    const float w = __expf(pmax[first + p] - mm);
+    l = fmaf(psum[first + p], w, l);
+    a = fmaf(pval[(first + p) * kHeadDim + d], w, a);
+  }
+  const float gv = Elem<ActT>::load(gate, out_idx);
+  Elem<ActT>::store(output, out_idx, (a / l) * sigmoid_gate(gv));
+}
+
+// ------------------------------------------------------------ launchers
+
+constexpr int kSingleHeads = 1, kSingleWaves = 16, kSingleUnroll = 2;
+constexpr int kPartHeads = 4, kPartWaves = 8, kPartUnroll = 2;
+
+template <typename ActT, typename CacheT>
+void launch_decode(const void *query, const void *key, const void *value, const void *gate,
+                   void *output, void *kv_cache, void *workspace, Qwen35AttentionShape shape,
+                   Qwen35KvCacheLayout layout, Qwen35OnlineDecodePlan plan,
+                   Qwen35OnlineDecodeWorkspaceLayout ws, const std::uint32_t *device_position,
+                   hipStream_t stream, bool partition_only) {
+  const bool head_major = layout == Qwen35KvCacheLayout::head_major;
+  const auto *q = static_cast<const ActT *>(query);
+  const auto *g = static_cast<const ActT *>(gate);
+  auto *out = static_cast<ActT *>(output);
+  auto *cache = static_cast<CacheT *>(kv_cache);
+  if (partition_only) {
+    require<Err>(plan.partition_tokens != 0, "partition-only decode needs a split-K plan");
+  } else {
+  append_decode_kernel<ActT, CacheT><<<4, 256, 0, stream>>>(
+      static_cast<const ActT *>(key), static_cast<const ActT *>(value), cache,
+      shape.max_context_tokens, shape.past_tokens, head_major, device_position);
+  check_launch<Err>("qwen35_online_attention_decode_append_cache");
+  }
+
+  // With a host position the path is known here, so kernels that would only
+  // early-exit are not enqueued.  With a device position every kernel of the
+  // plan is enqueued and selects itself on-device (graph-capture safe).
+  const std::size_t host_ctx = shape.past_tokens + 1;
+  const bool dynamic = device_position != nullptr;
+  const bool single = plan.resolved_mode == Qwen35DecodeAttentionMode::single_block;
+  if (!partition_only && (dynamic || single || host_ctx < plan.split_k_threshold_tokens)) {
+    decode_single_block_kernel<ActT, CacheT, kSingleHeads, kSingleWaves, kSingleUnroll>
+        <<<kQueryHeads / kSingleHeads, kSingleWaves * 64, 0, stream>>>(
+            q, g, out, cache, shape.max_context_tokens, shape.past_tokens, head_major,
+            device_position, plan.split_k_threshold_tokens);
+    check_launch<Err>("qwen35_online_attention_decode_gfx950_hd256");
+  }
+  if (single) return;
+  if (!dynamic && host_ctx < plan.split_k_threshold_tokens) return;
+
+  const std::size_t max_partitions = ceil_div(shape.max_context_tokens, plan.partition_tokens,
+                                              "online decode maximum partition capacity overflow");
+  const std::size_t units = kQueryHeads / kPartHeads;
+  const int grid = grid_dim(checked_mul<Err>(units, plan.active_partition_capacity,
+                                             "online decode partition grid dimension overflow"),
+                            "online decode partition grid dimension overflow");
+  auto *bytes = static_cast<std::byte *>(workspace);
+  auto *pmax = reinterpret_cast<float *>(bytes + ws.max_offset_bytes);
+  auto *psum = reinterpret_cast<float *>(bytes + ws.sum_offset_bytes);
+  auto *pval = reinterpret_cast<float *>(bytes + ws.value_offset_bytes);
+  decode_partition_kernel<ActT, CacheT, kPartHeads, kPartWaves, kPartUnroll>
+      <<<grid, kPartWaves * 64, 0, stream>>>(
+          q, cache, pmax, psum, pval, shape.max_context_tokens, shape.past_tokens, head_major,
+          plan.active_partition_capacity, max_partitions, plan.partition_tokens,
+          plan.split_k_threshold_tokens, device_position);
+  check_launch<Err>(plan.partition_tokens == 256
+                        ? "qwen35_online_attention_decode_split_k_256_partition"
+                        : "qwen35_online_attention_decode_split_k_512_partition");
+  decode_merge_kernel<ActT><<<kQueryHeads, 256, 0, stream>>>(
+      g, out, pmax, psum, pval, shape.max_context_tokens, shape.past_tokens,
+      plan.partition_tokens, max_partitions, plan.active_partition_capacity,
+      plan.split_k_threshold_tokens, device_position);
+  check_launch<Err>("qwen35_online_attention_decode_split_k_merge");
+}
+
+void require_aligned16(const void *p, const char *message) {
+  require<Err>((reinterpret_cast<std::uintptr_t>(p) & 15u) == 0, message);
+}
+
+} // namespace
+
+// ------------------------------------------------------------- plan API
+
+Qwen35OnlineDecodePlan qwen35_online_decode_plan(Qwen35AttentionShape shape,
+                                                 Qwen35DecodeAttentionMode requested,
+                                                 std::size_t context_tokens) {
+  require<Err>(shape.max_context_tokens != 0, "online decode plan maximum context tokens is zero");
+  require<Err>(context_tokens != 0, "online decode plan context tokens is zero");
+  require<Err>(context_tokens <= shape.max_context_tokens,
+               "online decode plan context tokens exceed maximum context");
+  const Qwen35DecodeAttentionMode resolved =
+      requested == Qwen35DecodeAttentionMode::auto_select ? kDefaultOnlineDecodeMode : requested;
+  const std::size_t partition = partition_tokens_for_mode(resolved);
+  if (partition != 0)
+    require<Err>(model_signature(shape), "split-K online decode requires the Qwen3.5 model signature");
+  const std::size_t bucket = context_bucket_tokens(shape, context_tokens);
+  if (partition == 0) return {resolved, 0, 0, bucket, 1};
+  return {resolved, partition, partition, bucket,
+          ceil_div(bucket, partition, "online decode active partition capacity overflow")};
+}
+
+Qwen35OnlineDecodeWorkspaceLayout
+qwen35_online_decode_workspace_layout(Qwen35AttentionShape shape,
+                                      Qwen35DecodeAttentionMode resolved_mode) {
+  require<Err>(resolved_mode != Qwen35DecodeAttentionMode::auto_select,
+               "online decode workspace mode must be resolved");
+  const std::size_t partition = partition_tokens_for_mode(resolved_mode);
+  if (partition == 0) return {};
+  require<Err>(model_signature(shape), "split-K online decode requires the Qwen3.5 model signature");
+  const std::size_t max_partitions = ceil_div(shape.max_context_tokens, partition,
+                                              "online decode maximum partition capacity overflow");
+  const std::size_t pc = checked_mul<Err>(shape.query_heads, max_partitions,
+                                          "online decode partial count overflow");
+  const std::size_t partial_bytes =
+      checked_mul<Err>(pc, sizeof(float), "online decode partial bytes overflow");
+  const std::size_t value_offset =
+      checked_mul<Err>(2, partial_bytes, "online decode value offset overflow");
+  const std::size_t value_bytes = checked_mul<Err>(
+      checked_mul<Err>(pc, shape.head_dim, "online decode partial value count overflow"),
+      sizeof(float), "online decode partial value bytes overflow");
+  return {pc, 0, partial_bytes, value_offset,
+          checked_add<Err>(value_offset, value_bytes, "online decode workspace bytes overflow")};
+}
+
+std::size_t qwen35_online_attention_workspace_bytes(Qwen35AttentionShape) noexcept { return 0; }
+
+// ------------------------------------------------------------ decode API
+namespace {
+// Validation order and messages: cpp/kernels/qwen35_online_attention.cu:1220-1314.
+void decode_impl(const void *query, const void *key, const void *value, const void *gate,
+                 void *output, void *kv_cache, std::size_t kv_cache_bytes, void *workspace,
+                 std::size_t workspace_bytes, Qwen35AttentionShape shape, RaftInferDataType act,
+                 Qwen35KvCacheDType cache_dtype, Qwen35KvCacheLayout layout,
+                 Qwen35OnlineDecodePlan plan, const std::uint32_t *device_position,
+                 hipStream_t stream, bool partition_only) {
+  require<Err>(query != nullptr, "online decode query pointer is null");
+  require<Err>(key != nullptr, "online decode key pointer is null");
+  require<Err>(value != nullptr, "online decode value pointer is null");
+  require<Err>(gate != nullptr, "online decode gate pointer is null");
+  require<Err>(output != nullptr, "online decode output pointer is null");
+  require<Err>(kv_cache != nullptr, "online decode KV cache pointer is null");
+  require<Err>(stream != nullptr, "online decode HIP stream is null");
+  require<Err>(online_decode_signature_supported(shape, act, cache_dtype, layout),
+               "unsupported online attention decode signature; select the "
+               "materialized implementation before allocation");
+  require<Err>(plan.resolved_mode != Qwen35DecodeAttentionMode::auto_select,
+               "online decode plan mode must be resolved");
+  const std::size_t expected_partition = partition_tokens_for_mode(plan.resolved_mode);
+  require<Err>(plan.partition_tokens == expected_partition,
+               "online decode plan partition size is inconsistent");
+  if (expected_partition == 0) {
+    require<Err>(plan.split_k_threshold_tokens == 0 && plan.active_partition_capacity == 1,
+                 "single-block online decode plan is inconsistent");
+    require<Err>(workspace_bytes == 0, "single-block online decode does not use split-K workspace");
+  } else {
+    require<Err>(plan.split_k_threshold_tokens == expected_partition,
+                 "split-K online decode threshold is inconsistent");
+    require<Err>(plan.context_bucket_tokens != 0 &&
+                     plan.context_bucket_tokens <= shape.max_context_tokens,
+                 "split-K online decode context bucket is invalid");
+    require<Err>(plan.active_partition_capacity ==
+                     ceil_div(plan.context_bucket_tokens, expected_partition,
+                              "online decode active partition capacity overflow"),
+                 "split-K online decode partition capacity is inconsistent");
+    require<Err>(device_position != nullptr || shape.past_tokens + 1 <= plan.context_bucket_tokens,
+                 "split-K online decode context exceeds the planned bucket");
+  }
+  const auto ws = qwen35_online_decode_workspace_layout(shape, plan.resolved_mode);
+  if (ws.bytes != 0) {
+    require<Err>(workspace != nullptr, "split-K online decode workspace is null");
+    require<Err>(workspace_bytes >= ws.bytes, "split-K online decode workspace is too small");
+  }
+  const std::size_t eb = cache_element_bytes_of(cache_dtype);
+  require<Err>(eb != 0, "unsupported online attention KV cache dtype");
+  require<Err>(layout_known(layout), "unsupported online attention KV cache layout");
+  const std::size_t required = checked_mul<Err>(
+      checked_mul<Err>(2,
+                       checked_mul<Err>(shape.max_context_tokens,
+                                        checked_mul<Err>(shape.kv_heads, shape.head_dim,
+                                                         "online decode cache shape overflow"),
+                                        "online decode cache shape overflow"),
+                       "online decode cache shape overflow"),
+      eb, "online decode cache byte size overflow");
+  require<Err>(kv_cache_bytes >= required, "online decode KV cache is too small");
+  // gfx950 kernels use 16-byte vector loads (an addition to the reference's
+  // checks; device allocations are 256-byte aligned).
+  require_aligned16(query, "online decode query must be 16-byte aligned");
+  require_aligned16(kv_cache, "online decode KV cache must be 16-byte aligned");
+
+  const bool f32_act = act == RAFTINFER_DTYPE_F32;
+  const bool f32_cache = cache_dtype == Qwen35KvCacheDType::f32;
+  if (f32_act && f32_cache)
+    launch_decode<float, float>(query, key, value, gate, output, kv_cache, workspace, shape,
+                                layout, plan, ws, device_position, stream, partition_only);
+  else if (f32_act)
+    launch_decode<float, bf16_bits>(query, key, value, gate, output, kv_cache, workspace, shape,
+                                    layout, plan, ws, device_position, stream, partition_only);
+  else if (f32_cache)
+    launch_decode<bf16_bits, float>(query, key, value, gate, output, kv_cache, workspace, shape,
+                                    layout, plan, ws, device_position, stream, partition_only);
+  else
+    launch_decode<bf16_bits, bf16_bits>(query, key, value, gate, output, kv_cache, workspace,
+                                        shape, layout, plan, ws, device_position, stream, partition_only);
+}
+
+} // namespace
+
+void qwen35_online_attention_decode(const void *query, const void *key, const void *value,
+                                    const void *gate, void *output, void *kv_cache,
+                                    std::size_t kv_cache_bytes, void *workspace,
+                                    std::size_t workspace_bytes, Qwen35AttentionShape shape,
+                                    RaftInferDataType act, Qwen35KvCacheDType cache_dtype,
+                                    Qwen35KvCacheLayout layout, Qwen35OnlineDecodePlan plan,
+                                    const std::uint32_t *device_position, hipStream_t stream) {
+  decode_impl(query, key, value, gate, output, kv_cache, kv_cache_bytes, workspace,
+              workspace_bytes, shape, act, cache_dtype, layout, plan, device_position, stream,
+              false);
+}
+
+void qwen35_online_attention_decode_partition_only(
+    const void *query, const void *key, const void *value, const void *gate, void *output,
+    void *kv_cache, std::size_t kv_cache_bytes, void *workspace, std::size_t workspace_bytes,
+    Qwen35AttentionShape shape, RaftInferDataType act, Qwen35KvCacheDType cache_dtype,
+    Qwen35KvCacheLayout layout, Qwen35OnlineDecodePlan plan, const std::uint32_t *device_position,
+    hipStream_t stream) {
+  decode_impl(query, key, value, gate, output, kv_cache, kv_cache_bytes, workspace,
+              workspace_bytes, shape, act, cache_dtype, layout, plan, device_position, stream,
+              true);
+}
+
+void qwen35_online_attention_decode(const void *query, const void *key, const void *value,
+                                    const void *gate, void *output, void *kv_cache,
+                                    std::size_t kv_cache_bytes, Qwen35AttentionShape shape,
+                                    RaftInferDataType act, Qwen35KvCacheDType cache_dtype,
+                                    Qwen35KvCacheLayout layout,
+                                    const std::uint32_t *device_position, hipStream_t stream) {
+  const auto plan = qwen35_online_decode_plan(shape, Qwen35DecodeAttentionMode::single_block,
+                                              shape.past_tokens + 1);
+  qwen35_online_attention_decode(query, key, value, gate, output, kv_cache, kv_cache_bytes,
+                                 nullptr, 0, shape, act, cache_dtype, layout, plan,
+                                 device_position, stream);
+}
+
+std::uint32_t qwen35_online_attention_consume_capacity_errors() {
+  unsigned int value = 0;
+  const unsigned int zero = 0;
+  require<Err>(hipDeviceSynchronize() == hipSuccess, "device synchronize failed");
+  require<Err>(hipMemcpyFromSymbol(&value, HIP_SYMBOL(g_capacity_errors), sizeof value) == hipSuccess,
+               "reading the capacity error counter failed");
+  require<Err>(hipMemcpyToSymbol(HIP_SYMBOL(g_capacity_errors), &zero, sizeof zero) == hipSuccess,
+               "clearing the capacity error counter failed");
+  return value;
+}
+
+// ------------------------------------------------------ batched decode
+namespace {
+
+constexpr std::size_t kBatchedPartition = 256;
+
+// Workgroup (sequence, head group, partition).  Sequences whose context is at
+// most single_max run single-block in partition 0 and write the gated output;
+// longer ones write partials for the merge.
+template <typename ActT, int NH, int WAVES, int U>
+__global__ __launch_bounds__(WAVES * 64) void batched_partition_kernel(
+    const ActT *__restrict__ query, const ActT *__restrict__ key, const ActT *__restrict__ value,
+    const ActT *__restrict__ gate, ActT *__restrict__ output, const std::byte *cache_base,
+    std::size_t cache_stride, std::size_t max_ctx, const std::uint32_t *__restrict__ lengths,
+    std::size_t max_partitions, std::size_t single_max, float *__restrict__ pmax,
+    float *__restrict__ psum, float *__restrict__ pval) {
+  __shared__ ScanShared<NH, WAVES> sh;
+  constexpr std::size_t units = kQueryHeads / NH;
+  const std::size_t seq = blockIdx.y;
+  const std::size_t unit = blockIdx.x / max_partitions;
+  const std::size_t partition = blockIdx.x % max_partitions;
+  const std::size_t ctx = lengths[seq];
+  if (ctx == 0 || ctx > max_ctx) return;
+  const bool single = ctx <= single_max;
+  const std::size_t begin = partition * kBatchedPartition;
+  if (single ? partition != 0 : begin >= ctx) return;
+  const std::size_t end = single ? ctx : (ctx < begin + kBatchedPartition ? ctx : begin + kBatchedPartition);
+  const auto *cache = reinterpret_cast<const bf16_bits *>(cache_base + seq * cache_stride);
+  const std::size_t first_head = unit * NH;
+  const std::size_t kv_head = first_head / kGroup;
+  const bf16_bits *k_plane = cache;
+  const bf16_bits *v_plane = cache + max_ctx * kKvHeads * kHeadDim;
+  const ActT *q = query + seq * kQueryHeads * kHeadDim;
+  scan_range<ActT, bf16_bits, NH, WAVES, U>(q, first_head, k_plane, v_plane, true, max_ctx,
+                                            kv_head, begin, end, sh);
+  __syncthreads();
+  for (int o = threadIdx.x; o < NH * kHeadDim; o += WAVES * 64) {
+    const int h = o / kHeadDim, d = o % kHeadDim;
+    float mm, l, a;
+    combine_waves(sh, h, d, mm, l, a);
+    const std::size_t head = first_head + h;
+    if (single) {
+      const std::size_t out_idx = (seq * kQueryHeads + head) * kHeadDim + d;
+      Elem<ActT>::store(output, out_idx, (a / l) * sigmoid_gate(Elem<ActT>::load(gate, out_idx)));
+    } else {
+      const std::size_t idx = (seq * kQueryHeads + head) * max_partitions + partition;
+      if (d == 0) {
+        pmax[idx] = mm * kLn2;
+        psum[idx] = l;
+      }
+      pval[idx * kHeadDim + d] = a;
+    }
+  }
+  (void)units;
+  (void)key;
+  (void)value;
+}
+
+template <typename ActT>
+__global__ __launch_bounds__(256) void batched_append_kernel(const ActT *__restrict__ key,
+                                                             const ActT *__restrict__ value,
+                                                             std::byte *cache_base,
+                                                             std::size_t cache_stride,
+                                                             std::size_t max_ctx,
+                                                             const std::uint32_t *lengths) {
+  const std::size_t seq = blockIdx.y;
+  const std::size_t ctx = lengths[seq];
+  if (ctx == 0 || ctx > max_ctx) return;
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  auto *cache = reinterpret_cast<bf16_bits *>(cache_base + seq * cache_stride);
+  const std::size_t idx = cache_row(true, ctx - 1, e >> 8, max_ctx) + (e & 255);
+  const std::size_t plane = max_ctx * kKvHeads * kHeadDim;
+  const std::size_t src = seq * kKvHeads * kHeadDim + e;
+  cache[idx] = f32_to_bf16(Elem<ActT>::load(key, src));
+  cache[plane + idx] = f32_to_bf16(Elem<ActT>::load(value, src));
+}
+
+template <typename ActT>
+__global__ __launch_bounds__(256) void batched_merge_kernel(
+    const ActT *__restrict__ gate, ActT *__restrict__ output, const float *__restrict__ pmax,
+    const float *__restrict__ psum, const float *__restrict__ pval,
+    const std::uint32_t *__restrict__ lengths, std::size_t max_ctx, std::size_t max_partitions,
+    std::size_t single_max) {
+  const std::size_t seq = blockIdx.y;
+  const std::size_t head = blockIdx.x;
+  const std::size_t ctx = lengths[seq];
+  if (ctx == 0 || ctx > max_ctx || ctx <= single_max) return;
+  const std::size_t active = ctx / kBatchedPartition + (ctx % kBatchedPartition ? 1 : 0);
+  const int d = threadIdx.x;
+  const std::size_t first = (seq * kQueryHeads + head) * max_partitions;
+  float mm = -INFINITY;
+  for (std::size_t p = 0; p < active; ++p) mm = fmaxf(mm, pmax[first + p]);
+  float l = 0.f, a = 0.f;
+  for (std::size_t p = 0; p < active; ++p) {
+    const float w = __expf(pmax[first + p] - mm);
+    l = fmaf(psum[first + p], w, l);
+    a = fmaf(pval[(first + p) * kHeadDim + d], w, a);
+  }
+  const std::size_t out_idx = (seq * kQueryHeads + head) * kHeadDim + d;
+  Elem<ActT>::store(output, out_idx, (a / l) * sigmoid_gate(Elem<ActT>::load(gate, out_idx)));
+}
+
+template <typename ActT>
+void launch_batched(const void *query, const void *key, const void *value, const void *gate,
+                    void *output, void *kv_cache, const std::uint32_t *lengths, void *workspace,
+                    Qwen35BatchedDecodeShape shape, hipStream_t stream) {
+  const std::size_t max_partitions = ceil_div_unchecked(shape.max_context_tokens, kBatchedPartition);
+  const std::size_t partials = shape.sequences * kQueryHeads * max_partitions;
+  auto *pmax = static_cast<float *>(workspace);
+  auto *psum = pmax + partials;
+  auto *pval = psum + partials;
+  auto *base = static_cast<std::byte *>(kv_cache);
+  const auto *q = static_cast<const ActT *>(query);
+  const auto *k = static_cast<const ActT *>(key);
+  const auto *v = static_cast<const ActT *>(value);
+  const auto *g = static_cast<const ActT *>(gate);
+  auto *out = static_cast<ActT *>(output);
+  const unsigned int seqs = static_cast<unsigned int>(shape.sequences);
+  batched_append_kernel<ActT><<<dim3(4, seqs), 256, 0, stream>>>(
+      k, v, base, shape.cache_stride_bytes, shape.max_context_tokens, lengths);
+  check_launch<Err>("qwen35_batched_decode_append_cache");
+  constexpr int NH = 4, WAVES = 8, U = 2;
+  const unsigned int gx = static_cast<unsigned int>((kQueryHeads / NH) * max_partitions);
+  batched_partition_kernel<ActT, NH, WAVES, U><<<dim3(gx, seqs), WAVES * 64, 0, stream>>>(
+      q, k, v, g, out, base, shape.cache_stride_bytes, shape.max_context_tokens, lengths,
+      max_partitions, shape.single_block_max_tokens, pmax, psum, pval);
+  check_launch<Err>("qwen35_batched_decode_partition");
+  batched_merge_kernel<ActT><<<dim3(kQueryHeads, seqs), 256, 0, stream>>>(
+      g, out, pmax, psum, pval, lengths, shape.max_context_tokens, max_partitions,
+      shape.single_block_max_tokens);
+  check_launch<Err>("qwen35_batched_decode_merge");
+}
+
+} // namespace
+
+std::size_t qwen35_batched_decode_workspace_bytes(Qwen35BatchedDecodeShape shape) {
+  require<Err>(shape.sequences != 0, "batched decode needs at least one sequence");
+  require<Err>(shape.max_context_tokens != 0, "batched decode maximum context is zero");
+  const std::size_t max_partitions = ceil_div_unchecked(shape.max_context_tokens, kBatchedPartition);
+  const std::size_t partials = checked_mul<Err>(
+      checked_mul<Err>(shape.sequences, kQueryHeads, "batched decode workspace overflow"),
+      max_partitions, "batched decode workspace overflow");
+  return checked_mul<Err>(checked_mul<Err>(partials, 2 + kHeadDim, "batched decode workspace overflow"),
+                          sizeof(float), "batched decode workspace overflow");
+}
+
+void qwen35_online_attention_decode_batched(const void *query, const void *key,
+                                            const void *value, const void *gate, void *output,
+                                            void *kv_cache, std::size_t kv_cache_bytes,
+                                            const std::uint32_t *context_lengths,
+                                            void *workspace, std::size_t workspace_bytes,
+                                            Qwen35BatchedDecodeShape shape, RaftInferDataType act,
+                                            hipStream_t stream) {
+  require<Err>(query && key && value && gate && output && kv_cache && context_lengths && workspace,
+               "batched decode pointer is null");
+  require<Err>(stream != nullptr, "batched decode HIP stream is null");
+  require<Err>(act == RAFTINFER_DTYPE_F32 || act == RAFTINFER_DTYPE_BF16,
+               "batched decode activation dtype must be f32 or bf16");
+  require<Err>(shape.sequences <= 65535, "batched decode supports at most 65535 sequences");
+  const std::size_t need_ws = qwen35_batched_decode_workspace_bytes(shape);
+  require<Err>(workspace_bytes >= need_ws, "batched decode workspace is too small");
+  const std::size_t per_seq = checked_mul<Err>(
+      checked_mul<Err>(2 * kKvHeads * kHeadDim, shape.max_context_tokens,
+                       "batched decode cache overflow"),
+      sizeof(bf16_bits), "batched decode cache overflow");
+  require<Err>(shape.cache_stride_bytes >= per_seq && shape.cache_stride_bytes % 16 == 0,
+               "batched decode cache stride is too small or not 16-byte aligned");
+  require<Err>(kv_cache_bytes >= checked_add<Err>(checked_mul<Err>(shape.sequences - 1,
+                                                                   shape.cache_stride_bytes,
+                                                                   "batched decode cache overflow"),
+                                                  per_seq, "batched decode cache overflow"),
+               "batched decode KV cache is too small");
+  require<Err>(ceil_div_unchecked(shape.max_context_tokens, kBatchedPartition) * 4 <= 0x7FFFFFFF,
+               "batched decode grid overflow");
+  require_aligned16(query, "batched decode query must be 16-byte aligned");
+  require_aligned16(kv_cache, "batched decode KV cache must be 16-byte aligned");
+  if (act == RAFTINFER_DTYPE_F32)
+    launch_batched<float>(query, key, value, gate, output, kv_cache, context_lengths, workspace,
+                          shape, stream);
+  else
+    launch_batched<bf16_bits>(query, key, value, gate, output, kv_cache, context_lengths,
+                              workspace, shape, stream);
+}
+
+} // namespace raftinfer::kernels

@@ -1,0 +1,164 @@
+// Shared host/device helpers for the gfx950 attention and gated-delta kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <limits>
+#include <stdexcept>
+#include <string>
+
+namespace raftinfer::amd {
+
+// ---------------------------------------------------------------- types
+using bf16_bits = std::uint16_t;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// ------------------------------------------------------- bf16 conversion
+// Round-to-nearest-even with quiet-NaN preservation, the rounding of
+// cpp/reference/bf16.hpp:16-32 (and of CUDA's __float2bfloat16_rn that the
+// reference kernels use for cache stores).
+__host__ __device__ __forceinline__ bf16_bits f32_to_bf16(float value) {
+  std::uint32_t bits;
+#if defined(__HIP_DEVICE_COMPILE__)
+  bits = __float_as_uint(value);
+#else
+  __builtin_memcpy(&bits, &value, sizeof bits);
+#endif
+  if ((bits & 0x7F800000u) == 0x7F800000u) {
+    const std::uint16_t sign_exp = static_cast<std::uint16_t>((bits >> 16) & 0xFF80u);
+    if ((bits & 0x007FFFFFu) == 0) return sign_exp;
+    std::uint16_t payload = static_cast<std::uint16_t>((bits >> 16) & 0x7Fu);
+    return static_cast<std::uint16_t>(sign_exp | (payload == 0 ? 1 : payload));
+  }
+  bits += 0x7FFFu + ((bits >> 16) & 1u);
+  return static_cast<std::uint16_t>(bits >> 16);
+}
+
+__host__ __device__ __forceinline__ float bf16_to_f32(bf16_bits b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __uint_as_float(static_cast<std::uint32_t>(b) << 16);
+#else
+  const std::uint32_t bits = static_cast<std::uint32_t>(b) << 16;
+  float f;
+  __builtin_memcpy(&f, &bits, sizeof f);
+  return f;
+#endif
+}
+
+// Low / high bf16 of a packed dword as float.
+__device__ __forceinline__ float bf16_lo(std::uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(std::uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+__device__ __forceinline__ std::uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<std::uint32_t>(f32_to_bf16(lo)) |
+         (static_cast<std::uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+// Element loads / stores from f32 or bf16 storage.
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static __device__ __forceinline__ float load(const float *p, std::size_t i) { return p[i]; }
+  static __device__ __forceinline__ void store(float *p, std::size_t i, float v) { p[i] = v; }
+};
+template <> struct Elem<bf16_bits> {
+  static __device__ __forceinline__ float load(const bf16_bits *p, std::size_t i) {
+    return bf16_to_f32(p[i]);
+  }
+  static __device__ __forceinline__ void store(bf16_bits *p, std::size_t i, float v) {
+    p[i] = f32_to_bf16(v);
+  }
+};
+template <> struct Elem<_Float16> {
+  static __device__ __forceinline__ float load(const _Float16 *p, std::size_t i) {
+    return static_cast<float>(p[i]);
+  }
+  static __device__ __forceinline__ void store(_Float16 *p, std::size_t i, float v) {
+    p[i] = static_cast<_Float16>(v);
+  }
+};
+
+// ------------------------------------------------- wavefront reductions
+// DPP row (16-lane) butterflies: quad_perm xor1 / xor2, row_half_mirror,
+// row_mirror.  After the four steps every lane of a 16-lane row holds the
+// row's total.
+template <int Ctrl> __device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), Ctrl, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // row_half_mirror
+constexpr int kDppMirror = 0x140;     // row_mirror
+
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp<kDppXor1>(x);
+  x += dpp<kDppXor2>(x);
+  x += dpp<kDppHalfMirror>(x);
+  x += dpp<kDppMirror>(x);
+  return x;
+}
+__device__ __forceinline__ float row16_max(float x) {
+  x = fmaxf(x, dpp<kDppXor1>(x));
+  x = fmaxf(x, dpp<kDppXor2>(x));
+  x = fmaxf(x, dpp<kDppHalfMirror>(x));
+  x = fmaxf(x, dpp<kDppMirror>(x));
+  return x;
+}
+// Exchange with lane ^ 16 / ^ 32 inside the wavefront (LDS crossbar, no
+// memory traffic).
+__device__ __forceinline__ float xor16(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401F));
+}
+__device__ __forceinline__ float xor32(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_ds_bpermute(((threadIdx.x ^ 32) & 63) << 2, __builtin_bit_cast(int, x)));
+}
+__device__ __forceinline__ float wave_sum(float x) {
+  x = row16_sum(x);
+  x += xor16(x);
+  x += xor32(x);
+  return x;
+}
+__device__ __forceinline__ float wave_max(float x) {
+  x = row16_max(x);
+  x = fmaxf(x, xor16(x));
+  x = fmaxf(x, xor32(x));
+  return x;
+}
+
+// ------------------------------------------------------ host utilities
+template <typename Error> inline void require(bool condition, const char *message) {
+  if (!condition) throw Error(message);
+}
+
+template <typename Error>
+inline std::size_t checked_mul(std::size_t a, std::size_t b, const char *message) {
+  require<Error>(a == 0 || b <= std::numeric_limits<std::size_t>::max() / a, message);
+  return a * b;
+}
+
+template <typename Error>
+inline std::size_t checked_add(std::size_t a, std::size_t b, const char *message) {
+  require<Error>(b <= std::numeric_limits<std::size_t>::max() - a, message);
+  return a + b;
+}
+
+inline std::size_t ceil_div_unchecked(std::size_t n, std::size_t d) {
+  return n / d + (n % d == 0 ? 0 : 1);
+}
+
+template <typename Error> inline void check_launch(const char *name) {
+  const hipError_t error = hipGetLastError();
+  if (error != hipSuccess) {
+    throw Error(std::string{name} + " launch failed: " + hipGetErrorString(error));
+  }
+}
+
+} // namespace raftinfer::amd

@@ -1,0 +1,810 @@
+// Gated DeltaNet (linear attention) for gfx950.
+//
+// Stages of qwen35_gated_delta (the reference's cpp/kernels/qwen35_delta.cu:
+// 675-755 runs the same four):
+//   1. conv_norm_kernel   causal depthwise conv (width W) + SiLU for every
+//                         q/k/v channel of a token, L2-norm of q/k heads
+//                         (q also x 1/sqrt(dk)), beta = sigmoid(b) and the log
+//                         decay g = A * softplus(a + dt_bias) per value head.
+//                         Fully parallel over (token, head vector).
+//      conv_state_kernel  shifts the W-1 token convolution history.
+//   2. recurrence, one of
+//      recurrent_kernel   lane = state column, rows split across 8 waves, the
+//                         fp32 state held in VGPRs over the token loop
+//                         (decode and short prefill);
+//      chunk_prep_kernel  per (value head, 64-token chunk), in parallel:
+//      + chunk_scan_kernel  UT/WY form of the chunk (fp32 MFMA 16x16x4):
+//                         A = beta_i e^{G_i-G_j} k_i.k_j (j<i), T = (I+A)^-1,
+//                         W = T diag(beta e^G) K, U = T diag(beta) V,
+//                         M = e^{G_i-G_j} q_i.k_j (j<=i); then per (value head,
+//                         16-column block) sequentially over chunks:
+//                         D = U - W S, O = e^G (Q S) + M D,
+//                         S' = e^{G_last} S + (e^{G_last-G} K)^T D.
+//                         Only differences G_i - G_j <= 0 are exponentiated.
+//   3. out_norm_kernel    RMSNorm(raw) * w * SiLU(z) -> activation dtype.
+// Host validation mirrors cpp/kernels/qwen35_delta.cu:26-135, :761-897.
+#include "common.hpp"
+#include "raftinfer_amd/qwen35_delta.hpp"
+
+#include <cmath>
+
+namespace raftinfer::kernels {
+namespace {
+
+using namespace raftinfer::amd;
+using Err = Qwen35DeltaError;
+
+constexpr float kQkNormEpsilon = 1.0e-6f;
+constexpr int kChunk = 64;
+constexpr int kColBlock = 16;
+constexpr int kChunkDim = 128;
+constexpr int kRecWaves = 8;
+constexpr std::size_t kChunkThreshold = 64;
+
+struct CheckedShape {
+  std::size_t key_size, value_size, conv_dim, token_stride, convolution_elements,
+      recurrent_elements, workspace_bytes;
+};
+
+std::size_t chunk_scratch_floats_per_token(std::size_t hv, std::size_t dk, std::size_t dv) {
+  return hv * (dk + dv + kChunk + 1);
+}
+
+// cpp/kernels/qwen35_delta.cu:67-135.  The workspace additionally holds
+// per-token beta / log-decay and the chunk scratch (still linear in tokens).
+CheckedShape validate_shape(const GatedDeltaShape &s) {
+  require<Err>(s.tokens > 0, "gated-delta tokens must be positive");
+  require<Err>(s.hidden_size > 0, "gated-delta hidden_size must be positive");
+  require<Err>(s.key_heads > 0, "gated-delta key_heads must be positive");
+  require<Err>(s.value_heads > 0, "gated-delta value_heads must be positive");
+  require<Err>(s.key_dim > 0, "gated-delta key_dim must be positive");
+  require<Err>(s.value_dim > 0, "gated-delta value_dim must be positive");
+  require<Err>(s.conv_width > 0, "gated-delta conv_width must be positive");
+  require<Err>(std::isfinite(s.epsilon) && s.epsilon >= 0.0f,
+               "gated-delta epsilon must be finite and non-negative");
+  require<Err>(s.value_heads % s.key_heads == 0,
+               "gated-delta value_heads must be divisible by key_heads");
+  const std::size_t key_size = checked_mul<Err>(s.key_heads, s.key_dim, "gated-delta key shape overflow");
+  const std::size_t value_size =
+      checked_mul<Err>(s.value_heads, s.value_dim, "gated-delta value shape overflow");
+  require<Err>(value_size == s.hidden_size,
+               "gated-delta value_heads * value_dim must equal hidden_size");
+  const std::size_t conv_dim =
+      checked_add<Err>(checked_mul<Err>(key_size, 2, "gated-delta convolution shape overflow"),
+                       value_size, "gated-delta convolution shape overflow");
+  const std::size_t token_stride = checked_add<Err>(
+      checked_add<Err>(conv_dim, checked_mul<Err>(s.value_heads, 2, "gated-delta input shape overflow"),
+                       "gated-delta input shape overflow"),
+      s.hidden_size, "gated-delta input shape overflow");
+  (void)checked_mul<Err>(s.tokens, token_stride, "gated-delta input shape overflow");
+  (void)checked_mul<Err>(s.tokens, s.hidden_size, "gated-delta output shape overflow");
+  (void)checked_mul<Err>(conv_dim, s.conv_width, "gated-delta convolution weight shape overflow");
+  const std::size_t conv_elems = checked_mul<Err>(conv_dim, s.conv_width - 1,
+                                                  "gated-delta convolution state shape overflow");
+  const std::size_t rec_elems =
+      checked_mul<Err>(value_size, s.key_dim, "gated-delta recurrent state shape overflow");
+  require<Err>(s.value_dim <= std::numeric_limits<std::size_t>::max() / 4 &&
+                   s.key_dim <= std::numeric_limits<std::size_t>::max() / 4,
+               "gated-delta workspace shape overflow");
+  const std::size_t per_token = checked_add<Err>(
+      checked_add<Err>(conv_dim, s.hidden_size, "gated-delta workspace shape overflow"),
+      checked_add<Err>(checked_mul<Err>(2, s.value_heads, "gated-delta workspace shape overflow"),
+                       checked_mul<Err>(s.value_heads, s.key_dim + s.value_dim + kChunk + 1,
+                                        "gated-delta workspace shape overflow"),
+                       "gated-delta workspace shape overflow"),
+      "gated-delta workspace shape overflow");
+  const std::size_t ws_bytes = checked_mul<Err>(
+      checked_mul<Err>(s.tokens, per_token, "gated-delta workspace shape overflow"), sizeof(float),
+      "gated-delta workspace byte size overflow");
+  const auto int_max = static_cast<std::size_t>(std::numeric_limits<int>::max());
+  require<Err>(s.tokens <= int_max, "gated-delta token count exceeds launch limit");
+  require<Err>(conv_dim <= int_max, "gated-delta convolution grid overflow");
+  require<Err>(s.key_heads * 2 <= int_max, "gated-delta Q/K normalization grid overflow");
+  require<Err>(s.value_heads <= 65535, "gated-delta recurrent grid overflow");
+  return {key_size, value_size, conv_dim, token_stride, conv_elems, rec_elems, ws_bytes};
+}
+
+void require_dtype(RaftInferDataType d) {
+  require<Err>(d == RAFTINFER_DTYPE_F32 || d == RAFTINFER_DTYPE_F16 || d == RAFTINFER_DTYPE_BF16,
+               "unsupported Qwen3.5 gated-delta dtype");
+}
+
+void require_weight_dtype(RaftInferDataType d, RaftInferDataType w) {
+  require<Err>(w == RAFTINFER_DTYPE_F32 || w == d ||
+                   (d == RAFTINFER_DTYPE_F32 && (w == RAFTINFER_DTYPE_F16 || w == RAFTINFER_DTYPE_BF16)),
+               "Qwen3.5 gated-delta weight dtype is incompatible with activations");
+}
+
+void require_aligned(const void *p, std::size_t a, const char *m) {
+  require<Err>(reinterpret_cast<std::uintptr_t>(p) % a == 0, m);
+}
+
+// cpp/kernels/qwen35_delta.cu:188-217
+void validate_policy(const GatedDeltaLaunchPolicy &p, const GatedDeltaShape &s) {
+  require<Err>(p.warps_per_block == 4, "gated-delta schedule requires four warps per block");
+  require<Err>(!p.transposed_boundary_state, "gated-delta transposed boundary state is not initialized");
+  switch (p.schedule) {
+  case GatedDeltaSchedule::register_resident_current: break;
+  case GatedDeltaSchedule::register_resident_prefill_sm120:
+    require<Err>(s.key_dim == 64 || s.key_dim == 128,
+                 "gated-delta sm120 schedule requires key dimension 64 or 128");
+    require<Err>(s.value_dim == s.key_dim,
+                 "gated-delta sm120 schedule requires matching value dimension");
+    break;
+  case GatedDeltaSchedule::register_resident_decode_sm120:
+    require<Err>(s.key_dim == 64 || s.key_dim == 128,
+                 "gated-delta sm120 schedule requires key dimension 64 or 128");
+    require<Err>(s.value_dim == s.key_dim,
+                 "gated-delta sm120 schedule requires matching value dimension");
+    require<Err>(s.tokens == 1, "gated-delta decode schedule requires exactly one token");
+    break;
+  default: throw Err("unknown gated-delta schedule");
+  }
+}
+
+// ---------------------------------------------------------- device math
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
+__device__ __forceinline__ float sigmoid(float v) { return 1.0f / (1.0f + __expf(-v)); }
+__device__ __forceinline__ float softplus(float v) {
+  if (v > 20.0f) return v;
+  if (v < -20.0f) return __expf(v);
+  return log1pf(__expf(v));
+}
+
+// Strided row source for q / k / v: element (t, head, i) at
+// base[t*row + head*head_stride + i] * scale.
+template <typename T> struct Src {
+  const T *base;
+  std::size_t row, head_stride;
+  float scale;
+  __device__ __forceinline__ float at(std::size_t t, std::size_t head, std::size_t i) const {
+    return Elem<T>::load(base, t * row + head * head_stride + i) * scale;
+  }
+};
+
+template <typename T> struct OutRows {
+  T *base; // [t][head][dv]
+  __device__ __forceinline__ void put(std::size_t idx, float v) const { Elem<T>::store(base, idx, v); }
+};
+
+// -------------------------------------------------------- stage 1 kernels
+
+// Block (token, vector): vector < Hk -> q head, < 2Hk -> k head, else v head.
+template <typename T, typename Wt>
+__global__ __launch_bounds__(256) void conv_norm_kernel(
+    const T *__restrict__ input, const Wt *__restrict__ conv_w, const float *__restrict__ conv_state,
+    const Wt *__restrict__ recurrent_a, const Wt *__restrict__ dt_bias, float *__restrict__ convolved,
+    float *__restrict__ beta, float *__restrict__ gdecay, std::size_t tokens, std::size_t stride,
+    std::size_t conv_dim, std::size_t hk, std::size_t hv, std::size_t dk, std::size_t dv,
+    std::size_t width) {
+  __shared__ float red[4];
+  const std::size_t t = blockIdx.x;
+  const std::size_t vec = blockIdx.y;
+  const bool is_q = vec < hk, is_k = !is_q && vec < 2 * hk;
+  const std::size_t base = is_q ? vec * dk : is_k ? hk * dk + (vec - hk) * dk : 2 * hk * dk + (vec - 2 * hk) * dv;
+  const std::size_t len = (is_q || is_k) ? dk : dv;
+  const std::size_t hist = width - 1;
+  float ss = 0.f;
+  float vals[4];
+  int n = 0;
+  for (std::size_t i = threadIdx.x; i < len; i += 256, ++n) {
+    const std::size_t ch = base + i;
+    const std::size_t wb = ch * width;
+    float sum = Elem<T>::load(input, t * stride + ch) * Elem<Wt>::load(conv_w, wb + hist);
+    for (std::size_t h = 0; h < hist; ++h) {
+      const std::size_t src = t + h;
+      const float prev = src < hist ? conv_state[ch * hist + src]
+                                    : Elem<T>::load(input, (src - hist) * stride + ch);
+      sum += prev * Elem<Wt>::load(conv_w, wb + h);
+    }
+    const float y = silu(sum);
+    if (n < 4) vals[n] = y;
+    ss += y * y;
+    if (!(is_q || is_k)) convolved[t * conv_dim + ch] = y;
+  }
+  if (is_q || is_k) {
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float total = red[0] + red[1] + red[2] + red[3];
+    float scale = 1.0f / sqrtf(total + kQkNormEpsilon);
+    if (is_q) scale *= 1.0f / sqrtf(static_cast<float>(dk));
+    n = 0;
+    for (std::size_t i = threadIdx.x; i < len; i += 256, ++n) {
+      float y = vals[n < 4 ? n : 3];
+      if (n >= 4) { // dims > 1024: recompute (never hit for Qwen3.5 shapes)
+        const std::size_t ch = base + i;
+        const std::size_t wb = ch * width;
+        float sum = Elem<T>::load(input, t * stride + ch) * Elem<Wt>::load(conv_w, wb + hist);
+        for (std::size_t h = 0; h < hist; ++h) {
+          const std::size_t src = t + h;
+          const float prev = src < hist ? conv_state[ch * hist + src]
+                                        : Elem<T>::load(input, (src - hist) * stride + ch);
+          sum += prev * Elem<Wt>::load(conv_w, wb + h);
+        }
+        y = silu(sum);
+      }
+      convolved[t * conv_dim + base + i] = y * scale;
+    }
+  }
+  if (vec == 0) {
+    for (std::size_t h = threadIdx.x; h < hv; h += 256) {
+      const float b = Elem<T>::load(input, t * stride + conv_dim + h);
+      const float a = Elem<T>::load(input, t * stride + conv_dim + hv + h);
+      beta[t * hv + h] = sigmoid(b);
+      gdecay[t * hv + h] = Elem<Wt>::load(recurrent_a, h) * softplus(a + Elem<Wt>::load(dt_bias, h));
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void conv_state_kernel(const T *__restrict__ input,
+                                                         float *__restrict__ conv_state,
+                                                         std::size_t tokens, std::size_t stride,
+                                                         std::size_t conv_dim, std::size_t width) {
+  const std::size_t ch = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (ch >= conv_dim) return;
+  const std::size_t hist = width - 1;
+  for (std::size_t h = 0; h < hist; ++h) {
+    const std::size_t src = tokens + h;
+    conv_state[ch * hist + h] = src < hist ? conv_state[ch * hist + src]
+                                           : Elem<T>::load(input, (src - hist) * stride + ch);
+  }
+}
+
+// ------------------------------------------------ stage 2a: recurrent
+// Block (value head, 64-column block).  Lane = column; wave w owns rows
+// [w*MAXR, (w+1)*MAXR).  Per token: S *= decay; kv = S^T k (cross-wave sum
+// in LDS); delta = beta (v - kv); S += k delta; o = S^T q (cross-wave sum).
+template <typename InT, typename OutT, int MAXR>
+__global__ __launch_bounds__(kRecWaves * 64) void recurrent_kernel(
+    Src<InT> qs, Src<InT> ks, Src<InT> vs, const float *__restrict__ beta,
+    const float *__restrict__ gdecay, float *__restrict__ state, OutT *__restrict__ out,
+    std::size_t tokens, std::size_t hk, std::size_t hv, std::size_t dk, std::size_t dv) {
+  __shared__ float red_kv[kRecWaves][64];
+  __shared__ float red_o[kRecWaves][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const std::size_t h = blockIdx.x;
+  const std::size_t kh = h % hk;
+  const std::size_t c = static_cast<std::size_t>(blockIdx.y) * 64 + lane;
+  const bool cvalid = c < dv;
+  float s[MAXR];
+  float *sh = state + h * dk * dv;
+#pragma unroll
+  for (int i = 0; i < MAXR; ++i) {
+    const std::size_t r = static_cast<std::size_t>(wave) * MAXR + i;
+    s[i] = (r < dk && cvalid) ? sh[r * dv + c] : 0.f;
+  }
+  for (std::size_t t = 0; t < tokens; ++t) {
+    const float b = beta[t * hv + h];
+    const float decay = __expf(gdecay[t * hv + h]);
+    float kr[MAXR];
+    float part = 0.f;
+#pragma unroll
+    for (int i = 0; i < MAXR; ++i) {
+      const std::size_t r = static_cast<std::size_t>(wave) * MAXR + i;
+      kr[i] = r < dk ? ks.at(t, kh, r) : 0.f;
+      s[i] *= decay;
+      part = fmaf(s[i], kr[i], part);
+    }
+    red_kv[wave][lane] = part;
+    __syncthreads();
+    float kv = 0.f;
+#pragma unroll
+    for (int w = 0; w < kRecWaves; ++w) kv += red_kv[w][lane];
+    const float delta = ((cvalid ? vs.at(t, h, c) : 0.f) - kv) * b;
+    float po = 0.f;
+#pragma unroll
+    for (int i = 0; i < MAXR; ++i) {
+      const std::size_t r = static_cast<std::size_t>(wave) * MAXR + i;
+      s[i] = fmaf(kr[i], delta, s[i]);
+      po = fmaf(s[i], r < dk ? qs.at(t, kh, r) : 0.f, po);
+    }
+    red_o[wave][lane] = po;
+    __syncthreads();
+    if (wave == 0 && cvalid) {
+      float o = 0.f;
+#pragma unroll
+      for (int w = 0; w < kRecWaves; ++w) o += red_o[w][lane];
+      Elem<OutT>::store(out, (t * hv + h) * dv + c, o);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < MAXR; ++i) {
+    const std::size_t r = static_cast<std::size_t>(wave) * MAXR + i;
+    if (r < dk && cvalid) sh[r * dv + c] = s[i];
+  }
+}
+
+// ------------------------------------------------- stage 2b: chunked
+// fp32 MFMA 16x16x4: lane l supplies A[l%16][l/16] and B[l/16][l%16] and
+// holds D[(l/16)*4 + r][l%16], r = 0..3.
+__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+constexpr int kLd = kChunkDim + 4; // LDS row stride for 128-wide rows
+constexpr int kLdC = kChunk + 4;   // LDS row stride for 64-wide rows
+constexpr int kLdB = kColBlock + 4;
+
+struct ChunkScratch {
+  float *w; // [hv][tokens][dk]
+  float *u; // [hv][tokens][dv]
+  float *m; // [hv][tokens][64]
+  float *g; // [hv][tokens] cumulative log decay within the chunk
+};
+
+struct PrepShared {
+  float k[kChunk][kLd];
+  float qv[kChunk][kLd];
+  float a[kChunk][kLdC];
+  float tm[kChunk][kLdC];
+  float g[kChunk];
+  float beta[kChunk];
+};
+
+template <typename InT>
+__global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> ks, Src<InT> vs,
+                                                         const float *__restrict__ beta,
+                                                         const float *__restrict__ gdecay,
+                                                         ChunkScratch scratch, std::size_t tokens,
+                                                         std::size_t hk, std::size_t hv) {
+  __shared__ PrepShared sh;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 15, lk = lane >> 4;
+  const std::size_t h = blockIdx.x;
+  const std::size_t kh = h % hk;
+  const std::size_t t0 = static_cast<std::size_t>(blockIdx.y) * kChunk;
+  const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
+
+  for (int e = tid; e < kChunk * kChunkDim; e += 256) {
+    const int i = e / kChunkDim, d = e % kChunkDim;
+    const bool ok = i < L;
+    sh.k[i][d] = ok ? ks.at(t0 + i, kh, d) : 0.f;
+    sh.qv[i][d] = ok ? qs.at(t0 + i, kh, d) : 0.f;
+  }
+  if (tid < kChunk) {
+    sh.beta[tid] = tid < L ? beta[(t0 + tid) * hv + h] : 0.f;
+    sh.g[tid] = tid < L ? gdecay[(t0 + tid) * hv + h] : 0.f;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float acc = 0.f;
+    for (int i = 0; i < kChunk; ++i) {
+      acc += sh.g[i];
+      sh.g[i] = acc;
+    }
+  }
+  __syncthreads();
+
+  // M = e^{G_i-G_j} (q_i . k_j), j <= i  -> scratch.m; wave w = row tile w.
+  for (int tj = 0; tj < 4; ++tj) {
+    floatx4 acc = floatx4{};
+    if (tj <= wave) {
+      for (int k0 = 0; k0 < kChunkDim; k0 += 4)
+        acc = mfma4(sh.qv[wave * 16 + lr][k0 + lk], sh.k[tj * 16 + lr][k0 + lk], acc);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = wave * 16 + lk * 4 + r, j = tj * 16 + lr;
+      const float v = (j <= i && i < L) ? acc[r] * __expf(sh.g[i] - sh.g[j]) : 0.f;
+      if (i < L) scratch.m[(h * tokens + t0 + i) * kChunk + j] = v;
+    }
+  }
+  // A = beta_i e^{G_i-G_j} (k_i . k_j), j < i  -> LDS.
+  for (int tj = 0; tj < 4; ++tj) {
+    floatx4 acc = floatx4{};
+    if (tj <= wave) {
+      for (int k0 = 0; k0 < kChunkDim; k0 += 4)
+        acc = mfma4(sh.k[wave * 16 + lr][k0 + lk], sh.k[tj * 16 + lr][k0 + lk], acc);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = wave * 16 + lk * 4 + r, j = tj * 16 + lr;
+      sh.a[i][j] = (j < i && i < L) ? sh.beta[i] * __expf(sh.g[i] - sh.g[j]) * acc[r] : 0.f;
+    }
+  }
+  __syncthreads();
+  // Q no longer needed: stage V.
+  for (int e = tid; e < kChunk * kChunkDim; e += 256) {
+    const int i = e / kChunkDim, d = e % kChunkDim;
+    sh.qv[i][d] = i < L ? vs.at(t0 + i, h, d) : 0.f;
+  }
+  // T = (I + A)^-1 by forward substitution, lane = column (wave 0).
+  if (wave == 0) {
+    float col[kChunk];
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+      float acc = i == lane ? 1.f : 0.f;
+#pragma unroll
+      for (int j = 0; j < i; ++j) acc = fmaf(-sh.a[i][j], col[j], acc);
+      col[i] = acc;
+      sh.tm[i][lane] = acc;
+    }
+  }
+  __syncthreads();
+  // W = T diag(beta e^G) K, U = T diag(beta) V: 4 x 8 output tiles.
+  for (int tile = wave; tile < 32; tile += 4) {
+    const int ti = tile >> 3, tn = tile & 7;
+    floatx4 aw = floatx4{}, au = floatx4{};
+    for (int j0 = 0; j0 < kChunk; j0 += 4) {
+      const int j = j0 + lk;
+      const float tmv = sh.tm[ti * 16 + lr][j];
+      const float bj = sh.beta[j];
+      aw = mfma4(tmv * bj * __expf(sh.g[j]), sh.k[j][tn * 16 + lr], aw);
+      au = mfma4(tmv * bj, sh.qv[j][tn * 16 + lr], au);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = ti * 16 + lk * 4 + r, d = tn * 16 + lr;
+      if (i < L) {
+        scratch.w[(h * tokens + t0 + i) * kChunkDim + d] = aw[r];
+        scratch.u[(h * tokens + t0 + i) * kChunkDim + d] = au[r];
+      }
+    }
+  }
+  if (tid < L) scratch.g[h * tokens + t0 + tid] = sh.g[tid];
+}
+
+struct ScanShared {
+  float wq[kChunk][kLd]; // W, then Q
+  float k[kChunk][kLd];
+  float s[kChunkDim][kLdB];
+  float d[kChunk][kLdB];
+  float u[kChunk][kLdB];
+  float m[kChunk][kLdC];
+  float g[kChunk];
+};
+
+// Block (value head, 16-column block), sequential over chunks.
+template <typename InT, typename OutT>
+__global__ __launch_bounds__(256) void chunk_scan_kernel(Src<InT> qs, Src<InT> ks,
+                                                         ChunkScratch scratch,
+                                                         float *__restrict__ state,
+                                                         OutT *__restrict__ out, std::size_t tokens,
+                                                         std::size_t hk, std::size_t hv) {
+  __shared__ ScanShared sh;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 15, lk = lane >> 4;
+  const std::size_t h = blockIdx.x;
+  const std::size_t kh = h % hk;
+  const int c0 = blockIdx.y * kColBlock;
+  float *sg = state + h * kChunkDim * kChunkDim;
+  for (int e = tid; e < kChunkDim * kColBlock; e += 256) {
+    const int r = e / kColBlock, c = e % kColBlock;
+    sh.s[r][c] = sg[r * kChunkDim + c0 + c];
+  }
+  for (std::size_t t0 = 0; t0 < tokens; t0 += kChunk) {
+    const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
+    __syncthreads();
+    for (int e = tid; e < kChunk * kChunkDim; e += 256) {
+      const int i = e / kChunkDim, d = e % kChunkDim;
+      const bool ok = i < L;
+      sh.wq[i][d] = ok ? scratch.w[(h * tokens + t0 + i) * kChunkDim + d] : 0.f;
+      sh.k[i][d] = ok ? ks.at(t0 + i, kh, d) : 0.f;
+    }
+    for (int e = tid; e < kChunk * kChunk; e += 256) {
+      const int i = e / kChunk, j = e % kChunk;
+      sh.m[i][j] = i < L ? scratch.m[(h * tokens + t0 + i) * kChunk + j] : 0.f;
+    }
+    for (int e = tid; e < kChunk * kColBlock; e += 256) {
+      const int i = e / kColBlock, c = e % kColBlock;
+      sh.u[i][c] = i < L ? scratch.u[(h * tokens + t0 + i) * kChunkDim + c0 + c] : 0.f;
+    }
+    if (tid < kChunk) sh.g[tid] = tid < L ? scratch.g[h * tokens + t0 + tid] : 0.f;
+    __syncthreads();
+    // D = U - W S (row tile = wave).
+    {
+      floatx4 acc = floatx4{};
+      for (int k0 = 0; k0 < kChunkDim; k0 += 4)
+        acc = mfma4(sh.wq[wave * 16 + lr][k0 + lk], sh.s[k0 + lk][lr], acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = wave * 16 + lk * 4 + r;
+        sh.d[i][lr] = i < L ? sh.u[i][lr] - acc[r] : 0.f;
+      }
+    }
+    __syncthreads();
+    for (int e = tid; e < kChunk * kChunkDim; e += 256) {
+      const int i = e / kChunkDim, d = e % kChunkDim;
+      sh.wq[i][d] = i < L ? qs.at(t0 + i, kh, d) : 0.f;
+    }
+    __syncthreads();
+    // O = e^G (Q S) + M D.
+    {
+      floatx4 qsacc = floatx4{}, md = floatx4{};
+      for (int k0 = 0; k0 < kChunkDim; k0 += 4)
+        qsacc = mfma4(sh.wq[wave * 16 + lr][k0 + lk], sh.s[k0 + lk][lr], qsacc);
+      for (int j0 = 0; j0 < kChunk; j0 += 4)
+        md = mfma4(sh.m[wave * 16 + lr][j0 + lk], sh.d[j0 + lk][lr], md);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = wave * 16 + lk * 4 + r;
+        if (i < L)
+          Elem<OutT>::store(out, ((t0 + i) * hv + h) * kChunkDim + c0 + lr,
+                            __expf(sh.g[i]) * qsacc[r] + md[r]);
+      }
+    }
+    // S' = e^{G_last} S + (e^{G_last - G_j} K_j)^T D: row tiles 2*wave, 2*wave+1.
+    const float glast = sh.g[L - 1];
+    floatx4 snew[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int rt = 2 * wave + tt;
+      floatx4 acc = floatx4{};
+      for (int j0 = 0; j0 < kChunk; j0 += 4) {
+        const int j = j0 + lk;
+        const float a = j < L ? sh.k[j][rt * 16 + lr] * __expf(glast - sh.g[j]) : 0.f;
+        acc = mfma4(a, sh.d[j][lr], acc);
+      }
+      const float gl = __expf(glast);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = fmaf(gl, sh.s[rt * 16 + lk * 4 + r][lr], acc[r]);
+      snew[tt] = acc;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sh.s[(2 * wave + tt) * 16 + lk * 4 + r][lr] = snew[tt][r];
+  }
+  __syncthreads();
+  for (int e = tid; e < kChunkDim * kColBlock; e += 256) {
+    const int r = e / kColBlock, c = e % kColBlock;
+    sg[r * kChunkDim + c0 + c] = sh.s[r][c];
+  }
+}
+
+// ----------------------------------------------------- stage 3 kernel
+// Block (token, value head): RMSNorm over dv, x weight, x SiLU(z)
+// (cpp/kernels/qwen35_delta.cu:578-621).
+template <typename T, typename Wt>
+__global__ __launch_bounds__(256) void out_norm_kernel(const T *__restrict__ input,
+                                                       const Wt *__restrict__ norm_w,
+                                                       const float *__restrict__ raw,
+                                                       T *__restrict__ output, std::size_t stride,
+                                                       std::size_t conv_dim, std::size_t hv,
+                                                       std::size_t dv, float eps) {
+  __shared__ float red[4];
+  const std::size_t t = blockIdx.x / hv, h = blockIdx.x % hv;
+  const std::size_t base = (t * hv + h) * dv;
+  float ss = 0.f;
+  for (std::size_t i = threadIdx.x; i < dv; i += 256) ss += raw[base + i] * raw[base + i];
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float total = red[0] + red[1] + red[2] + red[3];
+  const float scale = rsqrtf(total / static_cast<float>(dv) + eps);
+  const std::size_t zb = t * stride + conv_dim + 2 * hv + h * dv;
+  for (std::size_t i = threadIdx.x; i < dv; i += 256) {
+    const float n = raw[base + i] * scale * Elem<Wt>::load(norm_w, i);
+    Elem<T>::store(output, base + i, n * silu(Elem<T>::load(input, zb + i)));
+  }
+}
+
+// ------------------------------------------------------------ launchers
+
+template <typename InT, typename OutT>
+void launch_recurrence(Src<InT> q, Src<InT> k, Src<InT> v, const float *beta, const float *g,
+                       float *state, OutT *out, ChunkScratch scratch, std::size_t tokens,
+                       std::size_t hk, std::size_t hv, std::size_t dk, std::size_t dv, bool chunked,
+                       hipStream_t stream) {
+  if (chunked) {
+    const dim3 pgrid{static_cast<unsigned>(hv), static_cast<unsigned>(ceil_div_unchecked(tokens, kChunk)), 1};
+    chunk_prep_kernel<InT><<<pgrid, 256, 0, stream>>>(q, k, v, beta, g, scratch, tokens, hk, hv);
+    check_launch<Err>("qwen35_gated_delta chunk preparation");
+    const dim3 sgrid{static_cast<unsigned>(hv), kChunkDim / kColBlock, 1};
+    chunk_scan_kernel<InT, OutT><<<sgrid, 256, 0, stream>>>(q, k, scratch, state, out, tokens, hk, hv);
+    check_launch<Err>("qwen35_gated_delta chunk scan");
+    return;
+  }
+  const dim3 grid{static_cast<unsigned>(hv), static_cast<unsigned>(ceil_div_unchecked(dv, 64)), 1};
+  if (dk <= kRecWaves * 16)
+    recurrent_kernel<InT, OutT, 16><<<grid, kRecWaves * 64, 0, stream>>>(q, k, v, beta, g, state, out,
+                                                                         tokens, hk, hv, dk, dv);
+  else
+    recurrent_kernel<InT, OutT, 32><<<grid, kRecWaves * 64, 0, stream>>>(q, k, v, beta, g, state, out,
+                                                                         tokens, hk, hv, dk, dv);
+  check_launch<Err>("qwen35_gated_delta register recurrent update");
+}
+
+bool use_chunked(const GatedDeltaShape &s, const GatedDeltaLaunchPolicy &p) {
+  if (s.key_dim != kChunkDim || s.value_dim != kChunkDim) return false;
+  if (p.schedule == GatedDeltaSchedule::register_resident_prefill_sm120) return true;
+  if (p.schedule == GatedDeltaSchedule::register_resident_decode_sm120) return false;
+  return s.tokens >= kChunkThreshold;
+}
+
+template <typename T, typename Wt>
+void launch_typed(const void *input, const void *conv_weight, const void *recurrent_a,
+                  const void *dt_bias, const void *norm_w, void *output, float *conv_state,
+                  float *rec_state, float *ws, const GatedDeltaShape &s, const CheckedShape &c,
+                  const GatedDeltaLaunchPolicy &policy, hipStream_t stream) {
+  const auto *in = static_cast<const T *>(input);
+  float *convolved = ws;
+  float *raw = convolved + s.tokens * c.conv_dim;
+  float *beta = raw + s.tokens * s.hidden_size;
+  float *gdecay = beta + s.tokens * s.value_heads;
+  ChunkScratch scratch;
+  scratch.w = gdecay + s.tokens * s.value_heads;
+  scratch.u = scratch.w + s.value_heads * s.tokens * s.key_dim;
+  scratch.m = scratch.u + s.value_heads * s.tokens * s.value_dim;
+  scratch.g = scratch.m + s.value_heads * s.tokens * kChunk;
+
+  const dim3 cgrid{static_cast<unsigned>(s.tokens), static_cast<unsigned>(2 * s.key_heads + s.value_heads), 1};
+  conv_norm_kernel<T, Wt><<<cgrid, 256, 0, stream>>>(
+      in, static_cast<const Wt *>(conv_weight), conv_state, static_cast<const Wt *>(recurrent_a),
+      static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, s.tokens, c.token_stride, c.conv_dim,
+      s.key_heads, s.value_heads, s.key_dim, s.value_dim, s.conv_width);
+  check_launch<Err>("qwen35_gated_delta batched convolution");
+  if (s.conv_width > 1) {
+    conv_state_kernel<T><<<static_cast<unsigned>(ceil_div_unchecked(c.conv_dim, 256)), 256, 0, stream>>>(
+        in, conv_state, s.tokens, c.token_stride, c.conv_dim, s.conv_width);
+    check_launch<Err>("qwen35_gated_delta convolution state update");
+  }
+  const Src<float> q{convolved, c.conv_dim, s.key_dim, 1.0f};
+  const Src<float> k{convolved + c.key_size, c.conv_dim, s.key_dim, 1.0f};
+  const Src<float> v{convolved + 2 * c.key_size, c.conv_dim, s.value_dim, 1.0f};
+  launch_recurrence<float, float>(q, k, v, beta, gdecay, rec_state, raw, scratch, s.tokens,
+                                  s.key_heads, s.value_heads, s.key_dim, s.value_dim,
+                                  use_chunked(s, policy), stream);
+  out_norm_kernel<T, Wt><<<static_cast<unsigned>(s.tokens * s.value_heads), 256, 0, stream>>>(
+      in, static_cast<const Wt *>(norm_w), raw, static_cast<T *>(output), c.token_stride, c.conv_dim,
+      s.value_heads, s.value_dim, s.epsilon);
+  check_launch<Err>("qwen35_gated_delta batched output normalization");
+}
+
+template <typename T>
+void launch_for_weights(RaftInferDataType wdt, const void *input, const void *conv_weight,
+                        const void *recurrent_a, const void *dt_bias, const void *norm_w,
+                        void *output, float *conv_state, float *rec_state, float *ws,
+                        const GatedDeltaShape &s, const CheckedShape &c,
+                        const GatedDeltaLaunchPolicy &policy, hipStream_t stream) {
+  if (wdt == RAFTINFER_DTYPE_F32)
+    launch_typed<T, float>(input, conv_weight, recurrent_a, dt_bias, norm_w, output, conv_state,
+                           rec_state, ws, s, c, policy, stream);
+  else if (wdt == RAFTINFER_DTYPE_F16)
+    launch_typed<T, _Float16>(input, conv_weight, recurrent_a, dt_bias, norm_w, output, conv_state,
+                              rec_state, ws, s, c, policy, stream);
+  else
+    launch_typed<T, bf16_bits>(input, conv_weight, recurrent_a, dt_bias, norm_w, output, conv_state,
+                               rec_state, ws, s, c, policy, stream);
+}
+
+} // namespace
+
+std::size_t qwen35_gated_delta_workspace_bytes(const GatedDeltaShape &shape) {
+  return validate_shape(shape).workspace_bytes;
+}
+
+// The chunked schedule is the gfx950 counterpart of the reference's prefill
+// candidate; auto selection (register_resident_current) picks chunked for
+// >= 64 tokens of 128-dim heads and the register recurrence otherwise.
+GatedDeltaLaunchPolicy qwen35_gated_delta_select_policy(const GatedDeltaShape &,
+                                                        std::size_t) noexcept {
+  return GatedDeltaLaunchPolicy{GatedDeltaSchedule::register_resident_current, 4, false};
+}
+
+GatedDeltaScheduleDiagnostic qwen35_gated_delta_schedule_diagnostic(const GatedDeltaShape &shape,
+                                                                    std::size_t bucket) noexcept {
+  const auto p = qwen35_gated_delta_select_policy(shape, bucket);
+  GatedDeltaScheduleDiagnostic d;
+  d.bucket_tokens = bucket;
+  d.key_dim = shape.key_dim;
+  d.value_dim = shape.value_dim;
+  d.candidate_schedule = bucket == 1 ? GatedDeltaSchedule::register_resident_decode_sm120
+                                     : GatedDeltaSchedule::register_resident_prefill_sm120;
+  d.schedule = p.schedule;
+  d.warps_per_block = p.warps_per_block;
+  d.transposed_boundary_state = p.transposed_boundary_state;
+  d.candidate_accepted = p.schedule != GatedDeltaSchedule::register_resident_current;
+  d.correctness_passed = false;
+  d.rejection_reason = "not_tuned";
+  return d;
+}
+
+void qwen35_gated_delta(const void *input, const void *conv_weight, const void *recurrent_a,
+                        const void *dt_bias, const void *norm_w, void *output, float *conv_state,
+                        float *rec_state, void *workspace, std::size_t workspace_bytes,
+                        GatedDeltaShape shape, RaftInferDataType dtype,
+                        RaftInferDataType weight_dtype, hipStream_t stream) {
+  qwen35_gated_delta(input, conv_weight, recurrent_a, dt_bias, norm_w, output, conv_state,
+                     rec_state, workspace, workspace_bytes, shape,
+                     qwen35_gated_delta_select_policy(shape, shape.tokens), dtype, weight_dtype,
+                     stream);
+}
+
+// Validation order and messages: cpp/kernels/qwen35_delta.cu:811-897.
+void qwen35_gated_delta(const void *input, const void *conv_weight, const void *recurrent_a,
+                        const void *dt_bias, const void *norm_w, void *output, float *conv_state,
+                        float *rec_state, void *workspace, std::size_t workspace_bytes,
+                        GatedDeltaShape shape, GatedDeltaLaunchPolicy policy,
+                        RaftInferDataType dtype, RaftInferDataType weight_dtype,
+                        hipStream_t stream) {
+  const CheckedShape c = validate_shape(shape);
+  validate_policy(policy, shape);
+  require_dtype(dtype);
+  require_weight_dtype(dtype, weight_dtype);
+  require<Err>(input != nullptr, "gated-delta input pointer is null");
+  require<Err>(conv_weight != nullptr, "gated-delta convolution weight pointer is null");
+  require<Err>(recurrent_a != nullptr, "gated-delta recurrent coefficient pointer is null");
+  require<Err>(dt_bias != nullptr, "gated-delta dt-bias pointer is null");
+  require<Err>(norm_w != nullptr, "gated-delta output norm weight pointer is null");
+  require<Err>(output != nullptr, "gated-delta output pointer is null");
+  require<Err>(c.convolution_elements == 0 || conv_state != nullptr,
+               "gated-delta convolution state pointer is null");
+  require<Err>(c.recurrent_elements == 0 || rec_state != nullptr,
+               "gated-delta recurrent state pointer is null");
+  require<Err>(workspace != nullptr, "gated-delta workspace pointer is null");
+  require<Err>(workspace_bytes >= c.workspace_bytes, "gated-delta workspace is too small");
+  const std::size_t da = dtype == RAFTINFER_DTYPE_F32 ? 4 : 2;
+  const std::size_t wa = weight_dtype == RAFTINFER_DTYPE_F32 ? 4 : 2;
+  require_aligned(input, da, "gated-delta input is not dtype-aligned");
+  require_aligned(conv_weight, wa, "gated-delta convolution weight is not dtype-aligned");
+  require_aligned(recurrent_a, wa, "gated-delta recurrent coefficient is not dtype-aligned");
+  require_aligned(dt_bias, wa, "gated-delta dt-bias weight is not dtype-aligned");
+  require_aligned(norm_w, wa, "gated-delta output norm weight is not dtype-aligned");
+  require_aligned(output, da, "gated-delta output is not dtype-aligned");
+  require_aligned(workspace, 4, "gated-delta workspace is not float-aligned");
+  require_aligned(rec_state, 4, "gated-delta recurrent state is not float-aligned");
+  if (c.convolution_elements != 0)
+    require_aligned(conv_state, 4, "gated-delta convolution state is not float-aligned");
+  require<Err>(stream != nullptr, "HIP stream is null");
+  // Register recurrence keeps at most 32 rows per lane across 8 waves.
+  require<Err>(shape.key_dim <= kRecWaves * 32, "gated-delta key_dim above 256 is not supported");
+
+  auto *ws = static_cast<float *>(workspace);
+  if (dtype == RAFTINFER_DTYPE_F32)
+    launch_for_weights<float>(weight_dtype, input, conv_weight, recurrent_a, dt_bias, norm_w, output,
+                              conv_state, rec_state, ws, shape, c, policy, stream);
+  else if (dtype == RAFTINFER_DTYPE_F16)
+    launch_for_weights<_Float16>(weight_dtype, input, conv_weight, recurrent_a, dt_bias, norm_w,
+                                 output, conv_state, rec_state, ws, shape, c, policy, stream);
+  else
+    launch_for_weights<bf16_bits>(weight_dtype, input, conv_weight, recurrent_a, dt_bias, norm_w,
+                                  output, conv_state, rec_state, ws, shape, c, policy, stream);
+}
+
+// ------------------------------------------------------- core-only entry
+std::size_t qwen35_gated_delta_core_workspace_bytes(GatedDeltaCoreShape s) {
+  require<Err>(s.tokens > 0 && s.key_heads > 0 && s.value_heads > 0 && s.key_dim > 0 && s.value_dim > 0,
+               "gated-delta core shape must be positive");
+  return checked_mul<Err>(
+      checked_mul<Err>(s.tokens, chunk_scratch_floats_per_token(s.value_heads, s.key_dim, s.value_dim),
+                       "gated-delta core workspace overflow"),
+      sizeof(float), "gated-delta core workspace overflow");
+}
+
+void qwen35_gated_delta_core(const void *q, const void *k, const void *v, const float *beta,
+                             const float *log_decay, float q_scale, float *state, void *output,
+                             void *workspace, std::size_t workspace_bytes, GatedDeltaCoreShape s,
+                             bool chunked, hipStream_t stream) {
+  require<Err>(q && k && v && beta && log_decay && state && output, "gated-delta core pointer is null");
+  require<Err>(stream != nullptr, "HIP stream is null");
+  require<Err>(s.value_heads % s.key_heads == 0, "gated-delta value_heads must be divisible by key_heads");
+  require<Err>(s.key_dim <= kRecWaves * 32, "gated-delta key_dim above 256 is not supported");
+  require<Err>(s.value_heads <= 65535 && s.tokens <= 0x7FFFFFFF, "gated-delta core grid overflow");
+  if (chunked) {
+    require<Err>(s.key_dim == kChunkDim && s.value_dim == kChunkDim,
+                 "chunked gated-delta requires key_dim = value_dim = 128");
+    require<Err>(workspace != nullptr && workspace_bytes >= qwen35_gated_delta_core_workspace_bytes(s),
+                 "gated-delta core workspace is too small");
+  }
+  const Src<bf16_bits> qs{static_cast<const bf16_bits *>(q), s.key_heads * s.key_dim, s.key_dim, q_scale};
+  const Src<bf16_bits> ks{static_cast<const bf16_bits *>(k), s.key_heads * s.key_dim, s.key_dim, 1.0f};
+  const Src<bf16_bits> vs{static_cast<const bf16_bits *>(v), s.value_heads * s.value_dim, s.value_dim, 1.0f};
+  ChunkScratch scratch{};
+  if (chunked) {
+    scratch.w = static_cast<float *>(workspace);
+    scratch.u = scratch.w + s.value_heads * s.tokens * s.key_dim;
+    scratch.m = scratch.u + s.value_heads * s.tokens * s.value_dim;
+    scratch.g = scratch.m + s.value_heads * s.tokens * kChunk;
+  }
+  launch_recurrence<bf16_bits, bf16_bits>(qs, ks, vs, beta, log_decay, state,
+                                          static_cast<bf16_bits *>(output), scratch, s.tokens,
+                                          s.key_heads, s.value_heads, s.key_dim, s.value_dim,
+                                          chunked, stream);
+}
+
+} // namespace raftinfer::kernels

@@ -1,0 +1,308 @@
+"""GPU parity of the gfx950 attention path against the CPU oracle.
+
+Mirrors the reference's cpp/tests/qwen35_cuda_attention_test.cu cases
+(decode in every layout / dtype, split-K boundary contexts with partial-state
+checks, the capacity guard, online prefill incl. causality and adversarial
+rescaling, the materialized path) plus the BASELINE shapes.  Gates:
+ * bf16 outputs: max-abs 1e-2 (or one bf16 ulp of the expected value) and
+   relative-L2 5e-3 against the fp32-accumulated oracle;
+ * reference-style cases: abs <= 2e-2 or rel <= 2e-2 elementwise;
+ * cache appends and split-K bookkeeping (which partials are written, where):
+   bit-exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import (HKV, HQ, D, assert_bf16_close, bf16, cache_index, close_enough, from_dev,
+                     make_cache, normal, read_cache, rng, to_dev)
+from oracle import pyoracle as orc
+from raftinfer_amd import ops
+
+pytestmark = pytest.mark.gpu
+S = ops.Qwen35AttentionShape
+TDT = {1: torch.float32, 3: torch.bfloat16}
+CDT = {0: torch.float32, 1: torch.bfloat16}
+
+
+def quant(a, dt):
+    return bf16(a) if dt in (3, 1) and dt is not None else a
+
+
+def decode_inputs(seed, ctx, heavy_rows=0.0):
+    """Past keys/values for positions 0..ctx-2 plus the new token's q/k/v/gate."""
+    r = rng(seed)
+    past_k, past_v = normal(r, ctx - 1, HKV, D), normal(r, ctx - 1, HKV, D)
+    if heavy_rows:
+        past_k[r.random(ctx - 1) < heavy_rows] *= 8.0
+    q, g = normal(r, HQ, D), normal(r, HQ, D)
+    k, v = normal(r, HKV, D), normal(r, HKV, D)
+    return past_k, past_v, q, k, v, g
+
+
+def run_decode(act, cdt, layout, ctx, max_ctx, mode=None, device_position=True, seed=0,
+               heavy_rows=0.0, ws_fill=None):
+    past_k, past_v, q, k, v, g = decode_inputs(seed, ctx, heavy_rows)
+    qa, ka, va, ga = (bf16(x) if act == 3 else x for x in (q, k, v, g))
+    cache_np = make_cache(past_k, past_v, layout, max_ctx)
+    if cdt == 1:
+        cache_np = bf16(cache_np)
+    cache = to_dev(cache_np, CDT[cdt])
+    out = torch.empty(HQ * D, device="cuda", dtype=TDT[act])
+    shape = S(1, HQ, HKV, D, max_ctx, ctx - 1)
+    ws = None
+    plan = None
+    if mode is not None:
+        plan = ops.qwen35_online_decode_plan(shape, mode, max_ctx)
+        nbytes = ops.qwen35_online_decode_workspace_layout(shape, plan[0])[4]
+        if nbytes:
+            ws = torch.full((nbytes,), ws_fill if ws_fill is not None else 0, device="cuda",
+                            dtype=torch.uint8)
+    pos = torch.tensor([ctx - 1], device="cuda", dtype=torch.int32) if device_position else None
+    ops.qwen35_online_attention_decode(to_dev(qa, TDT[act]), to_dev(ka, TDT[act]),
+                                       to_dev(va, TDT[act]), to_dev(ga, TDT[act]), out, cache, ws,
+                                       shape, act, cdt, layout, plan=plan, device_position=pos)
+    torch.cuda.synchronize()
+    keys = np.concatenate([past_k, ka[None]])
+    vals = np.concatenate([past_v, va[None]])
+    if cdt == 1:
+        keys, vals = bf16(keys), bf16(vals)
+    expect = orc.attention_core(qa[None], keys, vals, ga[None], ctx - 1)[0]
+    return from_dev(out).reshape(HQ, D), expect, from_dev(cache), keys, vals, ws, plan
+
+
+def test_decode_cfg1_single_block_ctx512(gpu):
+    # ctx 512, bf16 head-major cache, single-block, no split.
+    out, expect, cache, keys, vals, _, _ = run_decode(3, 1, 1, 512, 512, mode=None,
+                                                      device_position=False, seed=11)
+    assert_bf16_close(out, bf16(expect), what="cfg1 decode")
+    ck, cv = read_cache(cache, 1, 512, 512)
+    assert np.array_equal(ck, keys) and np.array_equal(cv, vals)  # append is bit-exact
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("act,cdt", [(1, 0), (1, 1), (3, 0), (3, 1)])
+@pytest.mark.parametrize("ctx", [32, 128, 512])
+def test_decode_layouts_and_dtypes(gpu, layout, act, cdt, ctx):
+    # cpp/tests/qwen35_cuda_attention_test.cu:1067-1076
+    for device_position in (True, False):
+        out, expect, cache, keys, vals, _, _ = run_decode(act, cdt, layout, ctx, ctx + 1,
+                                                          mode=1, device_position=device_position,
+                                                          seed=ctx + layout)
+        assert close_enough(out, expect), (layout, act, cdt, ctx)
+        ck, cv = read_cache(cache, layout, ctx, ctx + 1)
+        assert np.array_equal(ck, keys) and np.array_equal(cv, vals)
+
+
+@pytest.mark.parametrize("ctx", [1, 255, 256, 257, 511, 512, 513, 777, 1024])
+def test_split_k_256_boundaries_and_partials(gpu, ctx):
+    # cpp/tests/qwen35_cuda_attention_test.cu:1078-1101, partials :883-957
+    max_ctx = 1025
+    out, expect, cache, keys, vals, ws, plan = run_decode(3, 1, 1, ctx, max_ctx, mode=2, seed=ctx,
+                                                          ws_fill=0xA5)
+    assert close_enough(out, expect)
+    assert_bf16_close(out, bf16(expect), what=f"split-256 ctx {ctx}")
+    wsb = ws.cpu().numpy()
+    if ctx < plan[2]:
+        assert np.all(wsb == 0xA5)  # below the threshold the workspace is untouched
+        return
+    lay = ops.qwen35_online_decode_workspace_layout(S(1, HQ, HKV, D, max_ctx, 0), 2)
+    f = wsb.view(np.float32)
+    maxp = -(-max_ctx // 256)
+    pm = f[lay[1] // 4:lay[1] // 4 + lay[0]].reshape(HQ, maxp)
+    ps = f[lay[2] // 4:lay[2] // 4 + lay[0]].reshape(HQ, maxp)
+    pv = f[lay[3] // 4:lay[3] // 4 + lay[0] * D].reshape(HQ, maxp, D)
+    em, es, ev = orc.decode_partials(bf16(decode_inputs(ctx, ctx)[2]), keys, vals, ctx, 256, maxp)
+    active = -(-ctx // 256)
+    sentinel = np.frombuffer(np.full(4, 0xA5, np.uint8).tobytes(), np.float32)[0]
+    assert np.all(pm[:, active:].view(np.uint32) == sentinel.view(np.uint32))  # untouched
+    assert close_enough(pm[:, :active], em.reshape(HQ, maxp)[:, :active])
+    assert close_enough(ps[:, :active], es.reshape(HQ, maxp)[:, :active])
+    assert close_enough(pv[:, :active], ev.reshape(HQ, maxp, D)[:, :active])
+
+
+@pytest.mark.parametrize("ctx", [513, 777])
+def test_split_k_512(gpu, ctx):
+    out, expect, *_ = run_decode(3, 1, 1, ctx, 1025, mode=3, seed=ctx + 5)
+    assert close_enough(out, expect)
+
+
+@pytest.mark.parametrize("ctx", [4096, 16384])
+def test_split_k_cfg2_long_context(gpu, ctx):
+    # auto (split-K 256), ~1% of K rows x8, host position.
+    out, expect, *_ = run_decode(3, 1, 1, ctx, ctx, mode=0, device_position=False, seed=ctx,
+                                 heavy_rows=0.01)
+    assert_bf16_close(out, bf16(expect), what=f"cfg2 ctx {ctx}")
+
+
+def test_single_block_equals_split(gpu):
+    a, *_ = run_decode(3, 1, 1, 1500, 2048, mode=1, seed=99)
+    b, *_ = run_decode(3, 1, 1, 1500, 2048, mode=2, seed=99)
+    assert_bf16_close(a, b, what="single vs split")
+
+
+def test_capacity_guard_reports_instead_of_trapping(gpu):
+    # cpp/tests/qwen35_cuda_attention_test.cu:1103-1164 (there: a device trap).
+    ops.consume_capacity_errors()
+    max_ctx = 1024
+    shape = S(1, HQ, HKV, D, max_ctx, 0)
+    plan = ops.qwen35_online_decode_plan(shape, 2, 256)
+    assert plan[3] == 512 and plan[4] == 2
+    nbytes = ops.qwen35_online_decode_workspace_layout(shape, 2)[4]
+    z = lambda n: torch.zeros(n, device="cuda", dtype=torch.bfloat16)
+    out = z(HQ * D)
+    cache = z(2 * max_ctx * HKV * D)
+    ws = torch.zeros(nbytes, device="cuda", dtype=torch.uint8)
+    pos = torch.tensor([512], device="cuda", dtype=torch.int32)
+    ops.qwen35_online_attention_decode(z(HQ * D), z(HKV * D), z(HKV * D), z(HQ * D), out, cache, ws,
+                                       shape, 3, 1, 1, plan=plan, device_position=pos)
+    assert ops.consume_capacity_errors() == 1
+    assert torch.isnan(out.float()).all()
+    assert ops.consume_capacity_errors() == 0
+
+
+def prefill_case(act, cdt, layout, T, hq, hkv, d, past, seed, q_scale=1.0):
+    r = rng(seed)
+    q, g = normal(r, T, hq, d), normal(r, T, hq, d)
+    k, v = normal(r, T, hkv, d), normal(r, T, hkv, d)
+    pk, pv = normal(r, past, hkv, d), normal(r, past, hkv, d)
+    return q, g, k, v, pk, pv
+
+
+def run_prefill(act, cdt, layout, T, hq, hkv, d, past, seed=0, inputs=None):
+    q, g, k, v, pk, pv = inputs if inputs is not None else prefill_case(act, cdt, layout, T, hq,
+                                                                         hkv, d, past, seed)
+    if act == 3:
+        q, g, k, v = (bf16(x) for x in (q, g, k, v))
+    max_ctx = past + T
+    cache_np = make_cache(pk, pv, layout, max_ctx, hkv, d)
+    if cdt == 1:
+        cache_np = bf16(cache_np)
+    cache = to_dev(cache_np, CDT[cdt])
+    out = torch.empty(T * hq * d, device="cuda", dtype=TDT[act])
+    shape = S(T, hq, hkv, d, max_ctx, past)
+    policy = ops.Qwen35AttentionLaunchPolicy(1, cdt, layout)
+    ops.qwen35_causal_attention(to_dev(q, TDT[act]), to_dev(k, TDT[act]), to_dev(v, TDT[act]),
+                                to_dev(g, TDT[act]), out, cache, None, shape, act, policy)
+    torch.cuda.synchronize()
+    keys = np.concatenate([pk, k]) if past else k
+    vals = np.concatenate([pv, v]) if past else v
+    if cdt == 1:
+        keys, vals = bf16(keys), bf16(vals)
+        if past:
+            keys[:past], vals[:past] = bf16(pk), bf16(pv)
+    expect = orc.attention_core(q, keys, vals, g, past)
+    return from_dev(out).reshape(T, hq, d), expect, from_dev(cache), keys, vals
+
+
+@pytest.mark.parametrize("T", [17, 128, 512])
+@pytest.mark.parametrize("past", [0, 111])
+def test_prefill_mfma_model_shape(gpu, T, past):
+    # BASELINE config 3 (PP128 / PP512) and the reference's {17,16,4,256,111} case.
+    out, expect, cache, keys, vals = run_prefill(3, 1, 1, T, HQ, HKV, D, past, seed=T + past)
+    assert_bf16_close(out, bf16(expect), what=f"prefill T={T} past={past}")
+    ck, cv = read_cache(cache, 1, past + T, past + T)
+    assert np.array_equal(ck, keys) and np.array_equal(cv, vals)
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("act,cdt", [(1, 0), (1, 1), (3, 0), (3, 1)])
+@pytest.mark.parametrize("case", [(4, 4, 2, 64, 0), (17, 16, 4, 256, 0), (17, 16, 4, 256, 111),
+                                  (9, 6, 3, 40, 5)])
+def test_prefill_layouts_dtypes_shapes(gpu, layout, act, cdt, case):
+    # cpp/tests/qwen35_cuda_attention_test.cu:753-766
+    T, hq, hkv, d, past = case
+    out, expect, *_ = run_prefill(act, cdt, layout, T, hq, hkv, d, past, seed=sum(case))
+    assert close_enough(out, expect), (layout, act, cdt, case)
+
+
+@pytest.mark.parametrize("act,cdt,layout", [(3, 1, 1), (1, 0, 0)])
+def test_prefill_causality(gpu, act, cdt, layout):
+    # cpp/tests/qwen35_cuda_attention_test.cu:688-705: the last token's K/V
+    # cannot change any earlier row (bit-identical).
+    T = 40
+    inputs = list(prefill_case(act, cdt, layout, T, HQ, HKV, D, 0, 5))
+    a, *_ = run_prefill(act, cdt, layout, T, HQ, HKV, D, 0, inputs=inputs)
+    inputs[2] = inputs[2].copy()
+    inputs[3] = inputs[3].copy()
+    inputs[2][-1] += 7.0
+    inputs[3][-1] -= 9.0
+    b, *_ = run_prefill(act, cdt, layout, T, HQ, HKV, D, 0, inputs=inputs)
+    assert np.array_equal(a[:-1], b[:-1])
+    assert not np.array_equal(a[-1], b[-1])
+
+
+@pytest.mark.parametrize("act,cdt", [(3, 1), (1, 0)])
+def test_prefill_adversarial_rescaling(gpu, act, cdt):
+    # cpp/tests/qwen35_cuda_attention_test.cu:709-750: scores -80 .. +80.
+    T, hq, hkv, d = 17, 4, 2, 64
+    q = np.zeros((T, hq, d), np.float32)
+    k = np.zeros((T, hkv, d), np.float32)
+    v = np.zeros((T, hkv, d), np.float32)
+    q[:, :, 0] = np.sqrt(d)
+    for t in range(T):
+        k[t, :, 0] = -80.0 + 10.0 * t
+        for h in range(hkv):
+            v[t, h] = 0.01 * (t + np.arange(d) + h)
+    g = np.zeros((T, hq, d), np.float32)
+    e = np.zeros((0, hkv, d), np.float32)
+    out, expect, *_ = run_prefill(act, cdt, 1, T, hq, hkv, d, 0, inputs=(q, g, k, v, e, e))
+    assert close_enough(out, expect)
+
+
+@pytest.mark.parametrize("act", [1, 2, 3])
+@pytest.mark.parametrize("T,past", [(17, 0), (1, 40), (5, 7)])
+def test_materialized_path(gpu, act, T, past):
+    # cpp/kernels/qwen35_attention.cu:463-563 (f32 token-major cache + logits workspace)
+    r = rng(T * 10 + act)
+    hq, hkv, d = 16, 4, 256
+    q, g = normal(r, T, hq, d), normal(r, T, hq, d)
+    k, v = normal(r, T, hkv, d), normal(r, T, hkv, d)
+    pk, pv = normal(r, past, hkv, d), normal(r, past, hkv, d)
+    tdt = {1: torch.float32, 2: torch.float16, 3: torch.bfloat16}[act]
+    enc = lambda a: from_dev(to_dev(a, tdt))
+    q, g, k, v = map(enc, (q, g, k, v))
+    max_ctx = past + T + 3
+    cache = to_dev(make_cache(pk, pv, 0, max_ctx, hkv, d), torch.float32)
+    shape = S(T, hq, hkv, d, max_ctx, past)
+    policy = ops.Qwen35AttentionLaunchPolicy(0, 0, 0)
+    ws = torch.empty(ops.qwen35_attention_workspace_bytes(shape, policy) // 4, device="cuda")
+    out = torch.empty(T * hq * d, device="cuda", dtype=tdt)
+    ops.qwen35_causal_attention(to_dev(q, tdt), to_dev(k, tdt), to_dev(v, tdt), to_dev(g, tdt), out,
+                                cache, ws, shape, act, policy)
+    torch.cuda.synchronize()
+    keys = np.concatenate([pk, k])
+    vals = np.concatenate([pv, v])
+    expect = orc.attention_core(q, keys, vals, g, past)
+    assert close_enough(from_dev(out).reshape(T, hq, d), expect)
+
+
+def test_batched_ragged_decode(gpu):
+    # BASELINE config 4 at reduced length: per-sequence oracle, mixed policies.
+    lengths = [1, 100, 511, 512, 513, 777, 2000, 4096]
+    B, max_ctx = len(lengths), 4096
+    r = rng(77)
+    per = 2 * max_ctx * HKV * D
+    cache_np = np.zeros(B * per, np.float32)
+    q, g = bf16(normal(r, B, HQ, D)), bf16(normal(r, B, HQ, D))
+    k, v = bf16(normal(r, B, HKV, D)), bf16(normal(r, B, HKV, D))
+    expects = []
+    for b, L in enumerate(lengths):
+        pk, pv = bf16(normal(r, L - 1, HKV, D)), bf16(normal(r, L - 1, HKV, D))
+        cache_np[b * per:(b + 1) * per] = make_cache(pk, pv, 1, max_ctx)
+        keys = np.concatenate([pk, k[b:b + 1]])
+        vals = np.concatenate([pv, v[b:b + 1]])
+        expects.append(orc.attention_core(q[b:b + 1], keys, vals, g[b:b + 1], L - 1)[0])
+    cache = to_dev(cache_np, torch.bfloat16)
+    lens = torch.tensor(lengths, device="cuda", dtype=torch.int32)
+    stride = per * 2
+    wsb = ops.qwen35_batched_decode_workspace_bytes(B, max_ctx, stride)
+    ws = torch.empty(wsb, device="cuda", dtype=torch.uint8)
+    out = torch.empty(B, HQ, D, device="cuda", dtype=torch.bfloat16)
+    bt = lambda a: to_dev(a, torch.bfloat16)
+    ops.qwen35_online_attention_decode_batched(bt(q), bt(k), bt(v), bt(g), out, cache, lens, ws,
+                                               max_ctx, stride)
+    torch.cuda.synchronize()
+    got = from_dev(out)
+    for b in range(B):
+        assert_bf16_close(got[b], bf16(expects[b]), what=f"batched seq {b} len {lengths[b]}")

@@ -1,0 +1,190 @@
+"""GPU parity of the gfx950 gated-delta path against the CPU oracle.
+
+Mirrors cpp/tests/qwen35_cuda_delta_test.cu (prefill lengths, continued
+prefill, decode after prefill, f32 auxiliary weights, f32 activations, the
+model-shape register path, both schedules) and BASELINE config 5 (chunked
+prefill T=512 in chunks of 64, then 32 recurrent decode steps).  Operands are
+quantised to the activation dtype before the fp32 oracle runs
+(cpp/tests/qwen35_cuda_delta_test.cu:258-276).  Gates: the reference's
+abs-or-rel 2e-2 for the full entry point; fp32 state within relative-L2 1e-4
+and bf16 outputs within max-abs 1e-2 / relative-L2 5e-3 for config 5.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_bf16_close, bf16, close_enough, from_dev, normal, rel_l2, rng, sequence, to_dev
+from oracle import pyoracle as orc
+from raftinfer_amd import ops
+
+pytestmark = pytest.mark.gpu
+TDT = {1: torch.float32, 2: torch.float16, 3: torch.bfloat16}
+
+
+def quantize(a, dt):
+    return from_dev(to_dev(a, TDT[dt]))
+
+
+def small_shape(T):
+    # cpp/tests/qwen35_cuda_delta_test.cu:194-205
+    return dict(tokens=T, hidden=28, hk=2, hv=4, dk=5, dv=7, width=3, eps=1e-6)
+
+
+def fixture_for(sh, seed=None):
+    cd = 2 * sh["hk"] * sh["dk"] + sh["hv"] * sh["dv"]
+    stride = cd + 2 * sh["hv"] + sh["hidden"]
+    if seed is None:  # the reference test's deterministic sequences (:236-248)
+        return dict(inp=sequence(sh["tokens"] * stride, 0.017, -0.03, 29, 17),
+                    cw=sequence(cd * sh["width"], 0.011, 0.04, 29, 17),
+                    a=sequence(sh["hv"], 0.03, -1.2, 29, 17),
+                    dt=sequence(sh["hv"], 0.025, -0.4, 29, 17),
+                    nw=sequence(sh["dv"], 0.02, 0.7, 29, 17))
+    r = rng(seed)
+    return dict(inp=normal(r, sh["tokens"] * stride), cw=normal(r, cd * sh["width"], scale=0.3),
+                a=-np.exp(normal(r, sh["hv"], scale=0.5)), dt=normal(r, sh["hv"]),
+                nw=normal(r, sh["dv"]))
+
+
+def run_gpu(sh, fx, dt, wdt, conv0=None, rec0=None, policy=None):
+    cd = 2 * sh["hk"] * sh["dk"] + sh["hv"] * sh["dv"]
+    shape = ops.GatedDeltaShape(sh["tokens"], sh["hidden"], sh["hk"], sh["hv"], sh["dk"], sh["dv"],
+                                sh["width"], sh["eps"])
+    conv = torch.zeros(cd * (sh["width"] - 1), device="cuda") if conv0 is None else to_dev(conv0, torch.float32)
+    rec = torch.zeros(sh["hv"] * sh["dk"] * sh["dv"], device="cuda") if rec0 is None else to_dev(rec0, torch.float32)
+    ws = torch.empty(ops.qwen35_gated_delta_workspace_bytes(shape) // 4, device="cuda")
+    out = torch.empty(sh["tokens"] * sh["hidden"], device="cuda", dtype=TDT[dt])
+    ops.qwen35_gated_delta(to_dev(fx["inp"], TDT[dt]), to_dev(fx["cw"], TDT[wdt]),
+                           to_dev(fx["a"], TDT[wdt]), to_dev(fx["dt"], TDT[wdt]),
+                           to_dev(fx["nw"], TDT[wdt]), out, conv if conv.numel() else None, rec, ws,
+                           shape, dt, wdt, policy=policy)
+    torch.cuda.synchronize()
+    return from_dev(out), from_dev(conv), from_dev(rec)
+
+
+def run_ref(sh, fx, dt, wdt, conv0=None, rec0=None):
+    cd = 2 * sh["hk"] * sh["dk"] + sh["hv"] * sh["dv"]
+    q = {k: quantize(v, dt if k == "inp" else wdt) for k, v in fx.items()}
+    conv0 = np.zeros(cd * (sh["width"] - 1), np.float32) if conv0 is None else conv0
+    rec0 = np.zeros(sh["hv"] * sh["dk"] * sh["dv"], np.float32) if rec0 is None else rec0
+    kw = {k: sh[k] for k in ("tokens", "hidden", "hk", "hv", "dk", "dv", "width", "eps")}
+    return orc.gated_delta_prefill(q["inp"], q["cw"], q["a"], q["dt"], q["nw"], conv0, rec0, **kw)
+
+
+def check(got, want):
+    for g, w in zip(got, want):
+        assert close_enough(g, w), np.abs(np.asarray(g) - np.asarray(w)).max()
+
+
+@pytest.mark.parametrize("dt", [2, 3])
+@pytest.mark.parametrize("T", [1, 2, 4, 17])
+def test_prefill_lengths(gpu, dt, T):
+    sh = small_shape(T)
+    fx = fixture_for(sh)
+    check(run_gpu(sh, fx, dt, dt), run_ref(sh, fx, dt, dt))
+
+
+def test_continued_prefill_and_decode(gpu):
+    # cpp/tests/qwen35_cuda_delta_test.cu:352-440
+    sh4, sh2, sh1 = small_shape(4), small_shape(2), small_shape(1)
+    f4 = fixture_for(sh4)
+    g4, w4 = run_gpu(sh4, f4, 3, 3), run_ref(sh4, f4, 3, 3)
+    check(g4, w4)
+    f2 = fixture_for(sh2)
+    f2["inp"] = f2["inp"] + 0.037
+    check(run_gpu(sh2, f2, 3, 3, g4[1], g4[2]), run_ref(sh2, f2, 3, 3, w4[1], w4[2]))
+    f1 = fixture_for(sh1, seed=5)
+    check(run_gpu(sh1, f1, 3, 3, g4[1], g4[2]), run_ref(sh1, f1, 3, 3, w4[1], w4[2]))
+
+
+def test_f32_auxiliary_weights_and_f32_activations(gpu):
+    sh = small_shape(4)
+    fx = fixture_for(sh)
+    check(run_gpu(sh, fx, 3, 1), run_ref(sh, fx, 3, 1))
+    check(run_gpu(sh, fx, 1, 1), run_ref(sh, fx, 1, 1))
+    check(run_gpu(sh, fx, 1, 3), run_ref(sh, fx, 1, 3))
+
+
+def test_saturation_edges(gpu):
+    # cpp/tests/qwen35_cuda_delta_test.cu:569-605: large |b|, |a| exercise the
+    # sigmoid / softplus branches.
+    sh = small_shape(4)
+    fx = fixture_for(sh)
+    cd = 2 * 2 * 5 + 4 * 7
+    stride = cd + 8 + 28
+    inp = fx["inp"].reshape(4, stride)
+    inp[:, cd:cd + 4] = [[30.0, -30.0, 0.0, 5.0]] * 4
+    inp[:, cd + 4:cd + 8] = [[40.0, -40.0, 20.5, -20.5]] * 4
+    fx["inp"] = inp.ravel()
+    check(run_gpu(sh, fx, 1, 1), run_ref(sh, fx, 1, 1))
+
+
+def model_shape(T):
+    return dict(tokens=T, hidden=4096, hk=16, hv=32, dk=128, dv=128, width=4, eps=1e-6)
+
+
+@pytest.mark.parametrize("T,schedule", [(3, 0), (1, 2), (17, 1), (128, 0), (150, 0)])
+def test_model_shape_schedules(gpu, T, schedule):
+    # cpp/tests/qwen35_cuda_delta_test.cu:631-650 plus both gfx950 schedules.
+    sh = model_shape(T)
+    fx = fixture_for(sh, seed=T)
+    r = rng(T + 1)
+    rec0 = normal(r, 32 * 128 * 128, scale=0.05)
+    conv0 = normal(r, 8192 * 3)
+    got = run_gpu(sh, fx, 3, 3, conv0, rec0, policy=ops.GatedDeltaLaunchPolicy(schedule))
+    want = run_ref(sh, fx, 3, 3, conv0, rec0)
+    check(got, want)
+    assert rel_l2(got[2], want[2]) < 1e-4
+
+
+def cfg5_inputs(T, seed):
+    """q, k ~ N(0,1) L2-normalised per head, v ~ N(0,1),
+    beta = sigmoid(N), g = -softplus(N); bf16 q/k/v."""
+    r = rng(seed)
+    q, k = normal(r, T, 16, 128), normal(r, T, 16, 128)
+    q = bf16(q / np.linalg.norm(q, axis=-1, keepdims=True))
+    k = bf16(k / np.linalg.norm(k, axis=-1, keepdims=True))
+    v = bf16(normal(r, T, 32, 128))
+    beta = (1 / (1 + np.exp(-normal(r, T, 32)))).astype(np.float32)
+    g = (-np.log1p(np.exp(normal(r, T, 32)))).astype(np.float32)
+    return q, k, v, beta, g
+
+
+def run_core(q, k, v, beta, g, state, chunked):
+    T = q.shape[0]
+    st = to_dev(state, torch.float32)
+    out = torch.empty(T, 32, 128, device="cuda", dtype=torch.bfloat16)
+    ws = torch.empty(ops.qwen35_gated_delta_core_workspace_bytes(T, 16, 32, 128, 128),
+                     device="cuda", dtype=torch.uint8)
+    bt = lambda a: to_dev(a, torch.bfloat16)
+    ops.qwen35_gated_delta_core(bt(q), bt(k), bt(v), to_dev(beta, torch.float32),
+                                to_dev(g, torch.float32), 1 / np.sqrt(128), st, out, ws, chunked)
+    torch.cuda.synchronize()
+    return from_dev(out), from_dev(st)
+
+
+def test_cfg5_chunked_prefill_then_32_decode_steps(gpu):
+    T = 512
+    q, k, v, beta, g = cfg5_inputs(T + 32, 2026)
+    s0 = np.zeros((32, 128, 128), np.float32)
+    want_o, want_s = orc.delta_core(q[:T], k[:T], v[:T], beta[:T], g[:T], 1 / np.sqrt(128), s0)
+    got_o, got_s = run_core(q[:T], k[:T], v[:T], beta[:T], g[:T], s0, chunked=True)
+    assert rel_l2(got_s, want_s) < 1e-4
+    assert_bf16_close(got_o, bf16(want_o), what="cfg5 chunked prefill")
+    s = got_s
+    ws_ = want_s
+    for t in range(T, T + 32):
+        sl = slice(t, t + 1)
+        wo, ws_ = orc.delta_core(q[sl], k[sl], v[sl], beta[sl], g[sl], 1 / np.sqrt(128), ws_)
+        go, s = run_core(q[sl], k[sl], v[sl], beta[sl], g[sl], s, chunked=False)
+        assert_bf16_close(go, bf16(wo), what=f"cfg5 decode step {t - T}")
+    assert rel_l2(s, ws_) < 1e-4
+
+
+def test_core_chunked_equals_recurrent(gpu):
+    T = 200
+    q, k, v, beta, g = cfg5_inputs(T, 7)
+    s0 = normal(rng(8), 32, 128, 128, scale=0.05)
+    a_o, a_s = run_core(q, k, v, beta, g, s0, chunked=True)
+    b_o, b_s = run_core(q, k, v, beta, g, s0, chunked=False)
+    assert rel_l2(a_s, b_s) < 1e-4
+    assert_bf16_close(a_o, b_o, what="chunked vs recurrent")
