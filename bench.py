@@ -64,29 +64,26 @@ def main():
     ev = lambda: torch.cuda.Event(enable_timing=True)
 
     def timed(fn, steps, warmup):
+        """Mean GPU time per call: the `steps` calls are captured into one HIP
+        graph (how a serving loop replays decode) and the replay is bracketed by
+        events on the launch stream, so host dispatch cost is excluded."""
         for i in range(warmup):
             fn(i)
         torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(steps):
+                fn(i)
+        graph.replay()
+        torch.cuda.synchronize()
         a, b = ev(), ev()
-        a.record()
-        for i in range(steps):
-            fn(i)
-        b.record()
+        a.record(stream)
+        graph.replay()
+        b.record(stream)
         torch.cuda.synchronize()
         return a.elapsed_time(b) / steps * 1e3  # us per call
 
-    def timed_each(fn, steps, warmup):
-        """Mean of per-launch event pairs (isolates one kernel's duration)."""
-        for i in range(warmup):
-            fn(i)
-        torch.cuda.synchronize()
-        pairs = [(ev(), ev()) for _ in range(steps)]
-        for i, (a, b) in enumerate(pairs):
-            a.record()
-            fn(i)
-            b.record()
-        torch.cuda.synchronize()
-        return sum(a.elapsed_time(b) for a, b in pairs) / steps * 1e3
+    timed_each = timed
 
     def rand_bf16(*shape):
         return torch.randn(*shape, device="cuda", dtype=torch.float32).to(torch.bfloat16)

@@ -6,6 +6,7 @@
 // cpp/kernels/qwen35_online_attention.cu:27-196 and :1071-1328.  Device work is
 // this build's own: one workgroup per (KV head, partition) serves the four
 // query heads of the GQA group, so each K/V byte is read from HBM once.
+#include "decode_mfma.hpp"
 #include "decode_scan.hpp"
 #include "raftinfer_amd/qwen35_online_attention.hpp"
 
@@ -194,9 +195,54 @@ __global__ __launch_bounds__(WAVES * 64) void decode_partition_kernel(
 }
 
 // Log-sum-exp merge over the active partitions of one query head plus the
-// sigmoid gate (cpp/kernels/qwen35_online_attention.cu:693-756).  A device
-// position needing more partitions than the plan's capacity writes NaN and
-// counts a capacity error instead of trapping.
+// sigmoid gate (cpp/kernels/qwen35_online_attention.cu:693-756).  The
+// partitions' max / sum are staged in LDS first so the value loads of all
+// partitions are independent.  A device position needing more partitions than
+// the plan's capacity writes NaN and counts a capacity error instead of
+// trapping.
+constexpr int kMergeChunk = 256;
+
+__device__ __forceinline__ void merge_head(const float *__restrict__ pmax,
+                                           const float *__restrict__ psum,
+                                           const float *__restrict__ pval, std::size_t first,
+                                           std::size_t active, float &l_out, float &a_out) {
+  __shared__ float w_sh[kMergeChunk];
+  __shared__ float red[4];
+  const int d = threadIdx.x;
+  float mm = -INFINITY;
+  for (std::size_t p = d; p < active; p += 256) mm = fmaxf(mm, pmax[first + p]);
+  mm = wave_max(mm);
+  if ((d & 63) == 0) red[d >> 6] = mm;
+  __syncthreads();
+  mm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float l = 0.f, a = 0.f;
+  for (std::size_t base = 0; base < active; base += kMergeChunk) {
+    const std::size_t n = active - base < kMergeChunk ? active - base : kMergeChunk;
+    __syncthreads();
+    if (static_cast<std::size_t>(d) < n) w_sh[d] = __expf(pmax[first + base + d] - mm);
+    __syncthreads();
+    float lp = 0.f;
+    if (static_cast<std::size_t>(d) < n) lp = psum[first + base + d] * w_sh[d];
+    l += lp;
+    const float *v = pval + (first + base) * kHeadDim + d;
+    std::size_t p = 0;
+    for (; p + 8 <= n; p += 8) {
+      float x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = v[(p + u) * kHeadDim];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) a = fmaf(x[u], w_sh[p + u], a);
+    }
+    for (; p < n; ++p) a = fmaf(v[p * kHeadDim], w_sh[p], a);
+  }
+  l = wave_sum(l);
+  __syncthreads();
+  if ((d & 63) == 0) red[d >> 6] = l;
+  __syncthreads();
+  l_out = red[0] + red[1] + red[2] + red[3];
+  a_out = a;
+}
+
 template <typename ActT>
 __global__ __launch_bounds__(256) void decode_merge_kernel(
     const ActT *__restrict__ gate, ActT *__restrict__ output, const float *__restrict__ pmax,
@@ -216,17 +262,94 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(
     Elem<ActT>::store(output, out_idx, __builtin_nanf(""));
     return;
   }
-  const std::size_t first = head * max_partitions;
-  float mm = -INFINITY;
-  for (std::size_t p = 0; p < active; ++p) mm = fmaxf(mm, pmax[first + p]);
-  float l = 0.f, a = 0.f;
-  for (std::size_t p = 0; p < active; ++p) {
-    const float w = __expf(pmax[first + p] - mm);
-    l = fmaf(psum[first + p], w, l);
-    a = fmaf(pval[(first + p) * kHeadDim + d], w, a);
-  }
+  float l, a;
+  merge_head(pmax, psum, pval, head * max_partitions, active, l, a);
   const float gv = Elem<ActT>::load(gate, out_idx);
   Elem<ActT>::store(output, out_idx, (a / l) * sigmoid_gate(gv));
+}
+
+// ---- bf16 activations + bf16 cache: MFMA scores, dims-sliced workgroups.
+constexpr int kSplitDs = 4, kSplitWaves = 8;
+constexpr int kSingleDs = 8, kSingleMfmaWaves = 8;
+
+// Copies the new token's K and V rows of kv_head into the cache (bf16 to
+// bf16, so the stored bits equal the RNE cast of the reference's append).
+__device__ __forceinline__ void append_rows(const DecodeMfmaArgs &a, std::size_t kv_head,
+                                            std::size_t pos) {
+  const int t = threadIdx.x;
+  if (t < kHeadDim / 8) {
+    const std::size_t row = cache_row(a.head_major, pos, kv_head, a.max_ctx) + 8 * t;
+    const std::size_t plane = a.max_ctx * kKvHeads * kHeadDim;
+    *reinterpret_cast<u32x4 *>(a.cache_rw + row) =
+        *reinterpret_cast<const u32x4 *>(a.key_new + kv_head * kHeadDim + 8 * t);
+    *reinterpret_cast<u32x4 *>(a.cache_rw + plane + row) =
+        *reinterpret_cast<const u32x4 *>(a.value_new + kv_head * kHeadDim + 8 * t);
+  }
+}
+
+template <int DS, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void decode_single_mfma_kernel(
+    DecodeMfmaArgs a, const bf16_bits *__restrict__ gate, bf16_bits *__restrict__ output,
+    std::size_t host_position, const std::uint32_t *device_position, std::size_t threshold) {
+  __shared__ DecodeMfmaShared<DS, WAVES> sh;
+  constexpr int DIMS = kHeadDim / DS;
+  const std::size_t position = read_position(device_position, host_position);
+  if (position >= a.max_ctx) return;
+  const std::size_t ctx = position + 1;
+  if (threshold != 0 && ctx >= threshold) return;
+  std::size_t kv_head;
+  int dq;
+  xcd_unit<DS>(blockIdx.x, kv_head, dq);
+  if (kv_head >= kKvHeads) return;
+  decode_mfma_scan<DS, WAVES>(a, kv_head, dq, 0, ctx, position, sh);
+  __syncthreads();
+  // The scan read the new row from key/value; the cache copy goes last so its
+  // load latency is not on the critical path.
+  if (dq == 0) append_rows(a, kv_head, position);
+  for (int o = threadIdx.x; o < kGroup * DIMS; o += WAVES * 64) {
+    const int h = o / DIMS, d = o % DIMS;
+    float mm, l, acc;
+    decode_mfma_combine(sh, h, d, mm, l, acc);
+    const std::size_t idx = (kv_head * kGroup + h) * kHeadDim + dq * DIMS + d;
+    output[idx] = f32_to_bf16((acc / l) * sigmoid_gate(bf16_to_f32(gate[idx])));
+  }
+}
+
+template <int DS, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void decode_split_mfma_kernel(
+    DecodeMfmaArgs a, float *__restrict__ pmax, float *__restrict__ psum,
+    float *__restrict__ pval, std::size_t host_position, const std::uint32_t *device_position,
+    std::size_t capacity, std::size_t max_partitions, std::size_t partition_tokens,
+    std::size_t threshold) {
+  __shared__ DecodeMfmaShared<DS, WAVES> sh;
+  constexpr int DIMS = kHeadDim / DS;
+  const std::size_t position = read_position(device_position, host_position);
+  if (position >= a.max_ctx) return;
+  const std::size_t ctx = position + 1;
+  if (ctx < threshold) return;
+  std::size_t unit;
+  int dq;
+  xcd_unit<DS>(blockIdx.x, unit, dq);
+  if (unit >= kKvHeads * capacity) return;
+  const std::size_t kv_head = unit / capacity;
+  const std::size_t partition = unit % capacity;
+  const std::size_t begin = partition * partition_tokens;
+  if (begin >= ctx) return;
+  const std::size_t end = ctx < begin + partition_tokens ? ctx : begin + partition_tokens;
+  decode_mfma_scan<DS, WAVES>(a, kv_head, dq, begin, end, position, sh);
+  __syncthreads();
+  if (dq == 0 && position >= begin && position < end) append_rows(a, kv_head, position);
+  for (int o = threadIdx.x; o < kGroup * DIMS; o += WAVES * 64) {
+    const int h = o / DIMS, d = o % DIMS;
+    float mm, l, acc;
+    decode_mfma_combine(sh, h, d, mm, l, acc);
+    const std::size_t idx = (kv_head * kGroup + h) * max_partitions + partition;
+    if (dq == 0 && d == 0) {
+      pmax[idx] = mm * kLn2;
+      psum[idx] = l;
+    }
+    pval[idx * kHeadDim + dq * DIMS + d] = acc;
+  }
 }
 
 // ------------------------------------------------------------ launchers
@@ -245,6 +368,59 @@ void launch_decode(const void *query, const void *key, const void *value, const 
   const auto *g = static_cast<const ActT *>(gate);
   auto *out = static_cast<ActT *>(output);
   auto *cache = static_cast<CacheT *>(kv_cache);
+  if constexpr (std::is_same_v<ActT, bf16_bits> && std::is_same_v<CacheT, bf16_bits>) {
+    const DecodeMfmaArgs args{q, static_cast<const bf16_bits *>(key),
+                              static_cast<const bf16_bits *>(value), cache, cache,
+                              shape.max_context_tokens, head_major};
+    const std::size_t host_ctx = shape.past_tokens + 1;
+    const bool dynamic = device_position != nullptr;
+    const bool single = plan.resolved_mode == Qwen35DecodeAttentionMode::single_block;
+    if (partition_only) require<Err>(!single, "partition-only decode needs a split-K plan");
+    if (!partition_only && (dynamic || single || host_ctx < plan.split_k_threshold_tokens)) {
+      decode_single_mfma_kernel<kSingleDs, kSingleMfmaWaves>
+          <<<xcd_grid<kSingleDs>(kKvHeads), kSingleMfmaWaves * 64, 0, stream>>>(
+              args, g, out, shape.past_tokens, device_position, plan.split_k_threshold_tokens);
+      check_launch<Err>("qwen35_online_attention_decode_gfx950_hd256");
+    }
+    if (single || (!dynamic && host_ctx < plan.split_k_threshold_tokens)) return;
+    const std::size_t max_partitions = ceil_div(shape.max_context_tokens, plan.partition_tokens,
+                                                "online decode maximum partition capacity overflow");
+    const std::size_t units = checked_mul<Err>(kKvHeads, plan.active_partition_capacity,
+                                               "online decode partition grid dimension overflow");
+    (void)grid_dim(checked_mul<Err>(units + 8, kSplitDs, "online decode partition grid dimension overflow"),
+                   "online decode partition grid dimension overflow");
+    auto *bytes = static_cast<std::byte *>(workspace);
+    auto *pmax = reinterpret_cast<float *>(bytes + ws.max_offset_bytes);
+    auto *psum = reinterpret_cast<float *>(bytes + ws.sum_offset_bytes);
+    auto *pval = reinterpret_cast<float *>(bytes + ws.value_offset_bytes);
+    // Slice the dims only while the partitions alone leave the 256 CUs idle.
+    if (units >= 192)
+      decode_split_mfma_kernel<1, kSplitWaves><<<xcd_grid<1>(units), kSplitWaves * 64, 0, stream>>>(
+          args, pmax, psum, pval, shape.past_tokens, device_position,
+          plan.active_partition_capacity, max_partitions, plan.partition_tokens,
+          plan.split_k_threshold_tokens);
+    else if (units >= 96)
+      decode_split_mfma_kernel<2, kSplitWaves><<<xcd_grid<2>(units), kSplitWaves * 64, 0, stream>>>(
+          args, pmax, psum, pval, shape.past_tokens, device_position,
+          plan.active_partition_capacity, max_partitions, plan.partition_tokens,
+          plan.split_k_threshold_tokens);
+    else
+      decode_split_mfma_kernel<kSplitDs, kSplitWaves>
+          <<<xcd_grid<kSplitDs>(units), kSplitWaves * 64, 0, stream>>>(
+              args, pmax, psum, pval, shape.past_tokens, device_position,
+              plan.active_partition_capacity, max_partitions, plan.partition_tokens,
+              plan.split_k_threshold_tokens);
+    check_launch<Err>(plan.partition_tokens == 256
+                          ? "qwen35_online_attention_decode_split_k_256_partition"
+                          : "qwen35_online_attention_decode_split_k_512_partition");
+    if (partition_only) return;
+    decode_merge_kernel<ActT><<<kQueryHeads, 256, 0, stream>>>(
+        g, out, pmax, psum, pval, shape.max_context_tokens, shape.past_tokens,
+        plan.partition_tokens, max_partitions, plan.active_partition_capacity,
+        plan.split_k_threshold_tokens, device_position);
+    check_launch<Err>("qwen35_online_attention_decode_split_k_merge");
+    return;
+  }
   if (partition_only) {
     require<Err>(plan.partition_tokens != 0, "partition-only decode needs a split-K plan");
   } else {
@@ -561,18 +737,66 @@ __global__ __launch_bounds__(256) void batched_merge_kernel(
   const std::size_t ctx = lengths[seq];
   if (ctx == 0 || ctx > max_ctx || ctx <= single_max) return;
   const std::size_t active = ctx / kBatchedPartition + (ctx % kBatchedPartition ? 1 : 0);
-  const int d = threadIdx.x;
-  const std::size_t first = (seq * kQueryHeads + head) * max_partitions;
-  float mm = -INFINITY;
-  for (std::size_t p = 0; p < active; ++p) mm = fmaxf(mm, pmax[first + p]);
-  float l = 0.f, a = 0.f;
-  for (std::size_t p = 0; p < active; ++p) {
-    const float w = __expf(pmax[first + p] - mm);
-    l = fmaf(psum[first + p], w, l);
-    a = fmaf(pval[(first + p) * kHeadDim + d], w, a);
-  }
-  const std::size_t out_idx = (seq * kQueryHeads + head) * kHeadDim + d;
+  float l, a;
+  merge_head(pmax, psum, pval, (seq * kQueryHeads + head) * max_partitions, active, l, a);
+  const std::size_t out_idx = (seq * kQueryHeads + head) * kHeadDim + threadIdx.x;
   Elem<ActT>::store(output, out_idx, (a / l) * sigmoid_gate(Elem<ActT>::load(gate, out_idx)));
+}
+
+// bf16 batched path: MFMA scores, dims-sliced workgroups, fused append.
+template <int DS, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void batched_mfma_kernel(
+    const bf16_bits *__restrict__ query, const bf16_bits *__restrict__ key,
+    const bf16_bits *__restrict__ value, const bf16_bits *__restrict__ gate,
+    bf16_bits *__restrict__ output, std::byte *cache_base, std::size_t cache_stride,
+    std::size_t max_ctx, const std::uint32_t *__restrict__ lengths, std::size_t max_partitions,
+    std::size_t single_max, float *__restrict__ pmax, float *__restrict__ psum,
+    float *__restrict__ pval) {
+  __shared__ DecodeMfmaShared<DS, WAVES> sh;
+  constexpr int DIMS = kHeadDim / DS;
+  const std::size_t seq = blockIdx.y;
+  const std::size_t ctx = lengths[seq];
+  if (ctx == 0 || ctx > max_ctx) return;
+  std::size_t unit;
+  int dq;
+  xcd_unit<DS>(blockIdx.x, unit, dq);
+  const bool single = ctx <= single_max;
+  std::size_t kv_head, partition = 0, begin = 0, end = ctx;
+  if (single) {
+    if (unit >= kKvHeads) return;
+    kv_head = unit;
+  } else {
+    if (unit >= kKvHeads * max_partitions) return;
+    kv_head = unit / max_partitions;
+    partition = unit % max_partitions;
+    begin = partition * kBatchedPartition;
+    if (begin >= ctx) return;
+    end = ctx < begin + kBatchedPartition ? ctx : begin + kBatchedPartition;
+  }
+  auto *cache = reinterpret_cast<bf16_bits *>(cache_base + seq * cache_stride);
+  const DecodeMfmaArgs a{query + seq * kQueryHeads * kHeadDim, key + seq * kKvHeads * kHeadDim,
+                         value + seq * kKvHeads * kHeadDim, cache, cache, max_ctx, true};
+  const std::size_t pos = ctx - 1;
+  decode_mfma_scan<DS, WAVES>(a, kv_head, dq, begin, end, pos, sh);
+  __syncthreads();
+  if (dq == 0 && pos >= begin && pos < end) append_rows(a, kv_head, pos);
+  for (int o = threadIdx.x; o < kGroup * DIMS; o += WAVES * 64) {
+    const int h = o / DIMS, d = o % DIMS;
+    float mm, l, acc;
+    decode_mfma_combine(sh, h, d, mm, l, acc);
+    const std::size_t head = seq * kQueryHeads + kv_head * kGroup + h;
+    if (single) {
+      const std::size_t idx = head * kHeadDim + dq * DIMS + d;
+      output[idx] = f32_to_bf16((acc / l) * sigmoid_gate(bf16_to_f32(gate[idx])));
+    } else {
+      const std::size_t idx = head * max_partitions + partition;
+      if (dq == 0 && d == 0) {
+        pmax[idx] = mm * kLn2;
+        psum[idx] = l;
+      }
+      pval[idx * kHeadDim + dq * DIMS + d] = acc;
+    }
+  }
 }
 
 template <typename ActT>
@@ -591,6 +815,19 @@ void launch_batched(const void *query, const void *key, const void *value, const
   const auto *g = static_cast<const ActT *>(gate);
   auto *out = static_cast<ActT *>(output);
   const unsigned int seqs = static_cast<unsigned int>(shape.sequences);
+  if constexpr (std::is_same_v<ActT, bf16_bits>) {
+    constexpr int DS = 1, WAVES = 8;
+    batched_mfma_kernel<DS, WAVES>
+        <<<dim3(xcd_grid<DS>(kKvHeads * max_partitions), seqs), WAVES * 64, 0, stream>>>(
+            q, k, v, g, out, base, shape.cache_stride_bytes, shape.max_context_tokens, lengths,
+            max_partitions, shape.single_block_max_tokens, pmax, psum, pval);
+    check_launch<Err>("qwen35_batched_decode_partition");
+    batched_merge_kernel<ActT><<<dim3(kQueryHeads, seqs), 256, 0, stream>>>(
+        g, out, pmax, psum, pval, lengths, shape.max_context_tokens, max_partitions,
+        shape.single_block_max_tokens);
+    check_launch<Err>("qwen35_batched_decode_merge");
+    return;
+  }
   batched_append_kernel<ActT><<<dim3(4, seqs), 256, 0, stream>>>(
       k, v, base, shape.cache_stride_bytes, shape.max_context_tokens, lengths);
   check_launch<Err>("qwen35_batched_decode_append_cache");

@@ -8,6 +8,7 @@
 #include <limits>
 #include <stdexcept>
 #include <string>
+#include <type_traits>
 
 namespace raftinfer::amd {
 
@@ -32,14 +33,13 @@ __host__ __device__ __forceinline__ bf16_bits f32_to_bf16(float value) {
 #else
   __builtin_memcpy(&bits, &value, sizeof bits);
 #endif
-  if ((bits & 0x7F800000u) == 0x7F800000u) {
-    const std::uint16_t sign_exp = static_cast<std::uint16_t>((bits >> 16) & 0xFF80u);
-    if ((bits & 0x007FFFFFu) == 0) return sign_exp;
-    std::uint16_t payload = static_cast<std::uint16_t>((bits >> 16) & 0x7Fu);
-    return static_cast<std::uint16_t>(sign_exp | (payload == 0 ? 1 : payload));
-  }
-  bits += 0x7FFFu + ((bits >> 16) & 1u);
-  return static_cast<std::uint16_t>(bits >> 16);
+  // Branch-free: the compiler turns both selects into v_cndmask.
+  const std::uint32_t hi = bits >> 16;
+  const std::uint32_t rounded = (bits + 0x7FFFu + (hi & 1u)) >> 16;
+  const bool nan_without_payload = (bits & 0x007FFFFFu) != 0 && (hi & 0x7Fu) == 0;
+  const std::uint32_t special = nan_without_payload ? (hi | 1u) : hi;
+  const bool inf_or_nan = (bits & 0x7F800000u) == 0x7F800000u;
+  return static_cast<bf16_bits>(inf_or_nan ? special : rounded);
 }
 
 __host__ __device__ __forceinline__ float bf16_to_f32(bf16_bits b) {
@@ -131,6 +131,16 @@ __device__ __forceinline__ float wave_max(float x) {
   x = fmaxf(x, xor16(x));
   x = fmaxf(x, xor32(x));
   return x;
+}
+
+// Orders a wave's own LDS writes before its later LDS reads by other lanes.
+// The LDS unit executes one wave's instructions in order, so only compiler
+// reordering must be prevented; a memory fence here would also wait for every
+// outstanding global store of the wave.
+__device__ __forceinline__ void wave_lds_order() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_wave_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 // ------------------------------------------------------ host utilities

@@ -1,0 +1,252 @@
+// bf16 decode attention core on gfx950 MFMA, used by the single-block,
+// split-K and batched decode kernels for bf16 activations and bf16 caches.
+//
+// Work split: a workgroup owns one KV head, one token range (a split-K
+// partition or the whole context) and one slice of DIMS = 256/DS output dims.
+// Every workgroup computes the full q.k scores of its range for the four query
+// heads of the GQA group (cheap on MFMA) but reads and accumulates only its
+// V slice, so a 256-token partition is shared by DS workgroups without any
+// cross-workgroup reduction or scratch memory: each writes its own dims of
+// the partial (max and sum are identical across the DS siblings).  Blocks are
+// numbered so the DS siblings of a partition land on the same XCD and share
+// its L2 (workgroups are dispatched round-robin over the 8 XCDs).
+//
+// Per wave, tokens are consumed 32 at a time:
+//   S[token][head] = v_mfma_f32_16x16x32_bf16(A = K rows, B = q^T) x 8 per 16 tokens
+//   online softmax in the exp2 domain (log2(e)/16 folded into the scale)
+//   O[head][dims] += p * V  on VALU (lane = dim pair x token phase)
+#pragma once
+
+#include "decode_scan.hpp"
+
+namespace raftinfer::amd {
+
+struct DecodeMfmaArgs {
+  const bf16_bits *query;   // [16][256] for this sequence
+  const bf16_bits *key_new; // [4][256] token appended at position ctx-1
+  const bf16_bits *value_new;
+  const bf16_bits *cache;   // K plane then V plane
+  bf16_bits *cache_rw;
+  std::size_t max_ctx;
+  bool head_major;
+};
+
+template <int DS, int WAVES> struct DecodeMfmaShared {
+  static constexpr int DIMS = kHeadDim / DS;
+  float p[WAVES][32][4];
+  float sc[WAVES][4];
+  float m[WAVES][4];
+  float l[WAVES][4];
+  float acc[WAVES][4][DIMS];
+};
+
+// PV lane mapping for a DIMS-wide slice: a lane owns VEC consecutive dims
+// (one 2*VEC-byte load per token) and one of TL token phases.
+template <int DIMS> struct PvMap {
+  static constexpr int VEC = DIMS / 32 > 2 ? (DIMS / 32 > 8 ? 8 : DIMS / 32) : 2;
+  static constexpr int DL = DIMS / VEC;
+  static constexpr int TL = 64 / DL;
+  static constexpr int TPL = 32 / TL;
+  static_assert(DL * VEC == DIMS && DL * TL == 64 && TPL * TL == 32, "bad PV map");
+};
+
+template <int VEC> struct VRow {
+  std::uint32_t w[VEC / 2];
+  __device__ __forceinline__ void load(const bf16_bits *p) {
+    if constexpr (VEC == 8) {
+      const u32x4 x = *reinterpret_cast<const u32x4 *>(p);
+      w[0] = x[0]; w[1] = x[1]; w[2] = x[2]; w[3] = x[3];
+    } else if constexpr (VEC == 4) {
+      const u32x2 x = *reinterpret_cast<const u32x2 *>(p);
+      w[0] = x[0]; w[1] = x[1];
+    } else {
+      w[0] = *reinterpret_cast<const std::uint32_t *>(p);
+    }
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < VEC / 2; ++i) w[i] = 0u;
+  }
+  __device__ __forceinline__ float get(int e) const {
+    return (e & 1) ? bf16_hi(w[e >> 1]) : bf16_lo(w[e >> 1]);
+  }
+};
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Scans tokens [begin, end) of kv_head for the dims slice dq; leaves
+// per-wave (m, l, acc) in sh.  Row `pos` (the token being appended) is read
+// from key_new / value_new instead of the cache.
+template <int DS, int WAVES>
+__device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::size_t kv_head,
+                                                 int dq, std::size_t begin, std::size_t end,
+                                                 std::size_t pos, DecodeMfmaShared<DS, WAVES> &sh) {
+  constexpr int DIMS = kHeadDim / DS;
+  using Map = PvMap<DIMS>;
+  constexpr int VEC = Map::VEC, DL = Map::DL, TL = Map::TL, TPL = Map::TPL;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n = lane & 15;  // head column of the score tile
+  const int kq = lane >> 4; // k-quarter of the MFMA operands
+  const int dl = lane % DL;
+  const int tl = lane / DL;
+  const float scale = kLog2e / 16.0f;
+  const std::size_t plane = a.max_ctx * kKvHeads * kHeadDim;
+  const bf16_bits *kplane = a.cache;
+  const bf16_bits *vplane = a.cache + plane;
+
+  // q^T as the B operand: lane holds head n, dims kb*32 + kq*8 .. +8.
+  bf16x8 qb[8];
+#pragma unroll
+  for (int kb = 0; kb < 8; ++kb) {
+    u32x4 w = u32x4{0u, 0u, 0u, 0u};
+    if (n < kGroup)
+      w = *reinterpret_cast<const u32x4 *>(a.query + (kv_head * kGroup + n) * kHeadDim + kb * 32 + kq * 8);
+    qb[kb] = __builtin_bit_cast(bf16x8, w);
+  }
+
+  float m_run = -INFINITY; // per head n (lanes with the same n agree)
+  float l_run = 0.f;       // per-lane partial sum for head n
+  float acc[4][VEC];
+#pragma unroll
+  for (int h = 0; h < 4; ++h)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[h][e] = 0.f;
+
+  for (std::size_t c0 = begin + static_cast<std::size_t>(wave) * 32; c0 < end;
+       c0 += static_cast<std::size_t>(WAVES) * 32) {
+    // Issue every load of the chunk first: K for the scores, V for the slice.
+    u32x4 kv[2][8];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const std::size_t tok = c0 + 16 * g + n;
+      const bf16_bits *row = tok == pos ? a.key_new + kv_head * kHeadDim
+                                        : kplane + cache_row(a.head_major, tok, kv_head, a.max_ctx);
+#pragma unroll
+      for (int kb = 0; kb < 8; ++kb)
+        kv[g][kb] = tok < end ? *reinterpret_cast<const u32x4 *>(row + kb * 32 + kq * 8)
+                              : u32x4{0u, 0u, 0u, 0u};
+    }
+    VRow<VEC> vv[TPL];
+#pragma unroll
+    for (int j = 0; j < TPL; ++j) {
+      const std::size_t tok = c0 + tl + TL * j;
+      const bf16_bits *row = tok == pos ? a.value_new + kv_head * kHeadDim
+                                        : vplane + cache_row(a.head_major, tok, kv_head, a.max_ctx);
+      if (tok < end)
+        vv[j].load(row + dq * DIMS + VEC * dl);
+      else
+        vv[j].zero();
+    }
+    // Scores: tile g holds S[token 16g + kq*4 + i][head n].
+    floatx4 s[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      s[g] = floatx4{};
+#pragma unroll
+      for (int kb = 0; kb < 8; ++kb)
+        s[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kv[g][kb]), qb[kb],
+                                                       s[g], 0, 0, 0);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const std::size_t tok = c0 + 16 * g + kq * 4 + i;
+        s[g][i] = tok < end ? s[g][i] * scale : -INFINITY;
+        mx = fmaxf(mx, s[g][i]);
+      }
+    mx = fmaxf(mx, xor16(mx));
+    mx = fmaxf(mx, xor32(mx));
+    const float m_new = fmaxf(m_run, mx);
+    const float sc = fast_exp2(m_run - m_new); // m_run = -inf -> 0
+    float psum = 0.f;
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = fast_exp2(s[g][i] - m_new);
+        psum += p;
+        if (n < kGroup) sh.p[wave][16 * g + kq * 4 + i][n] = p;
+      }
+    l_run = l_run * sc + psum;
+    m_run = m_new;
+    if (lane < kGroup) sh.sc[wave][lane] = sc;
+    wave_lds_order();
+    float scl[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) scl[h] = sh.sc[wave][h];
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[h][e] *= scl[h];
+#pragma unroll
+    for (int j = 0; j < TPL; ++j) {
+      const float4 p4 = *reinterpret_cast<const float4 *>(&sh.p[wave][tl + TL * j][0]);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float v = vv[j].get(e);
+        acc[0][e] = fmaf(p4.x, v, acc[0][e]);
+        acc[1][e] = fmaf(p4.y, v, acc[1][e]);
+        acc[2][e] = fmaf(p4.z, v, acc[2][e]);
+        acc[3][e] = fmaf(p4.w, v, acc[3][e]);
+      }
+    }
+    wave_lds_order();
+  }
+  // Sum l over the four row-quarters (lanes n, n+16, n+32, n+48).
+  float l_tot = l_run + xor16(l_run);
+  l_tot += xor32(l_tot);
+  // Sum acc over the token phases (lanes differing in bits >= log2(DP)).
+#pragma unroll
+  for (int off = DL; off < 64; off <<= 1)
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[h][e] += __shfl_xor(acc[h][e], off);
+  if (lane < kGroup) {
+    sh.m[wave][lane] = m_run;
+    sh.l[wave][lane] = l_tot;
+  }
+  if (tl == 0) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) sh.acc[wave][h][VEC * dl + e] = acc[h][e];
+  }
+}
+
+template <int DS, int WAVES>
+__device__ __forceinline__ void decode_mfma_combine(const DecodeMfmaShared<DS, WAVES> &sh, int h,
+                                                    int d, float &m_out, float &l_out,
+                                                    float &a_out) {
+  float mm = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) mm = fmaxf(mm, sh.m[w][h]);
+  float l = 0.f, acc = 0.f;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) {
+    const float wgt = fast_exp2(sh.m[w][h] - mm);
+    l = fmaf(sh.l[w][h], wgt, l);
+    acc = fmaf(sh.acc[w][h][d], wgt, acc);
+  }
+  m_out = mm;
+  l_out = l;
+  a_out = acc;
+}
+
+// Maps a block id to (unit, dims slice) so the DS slices of one unit share
+// an XCD: unit t's slices are blocks ((t/8)*DS + dq)*8 + t%8.
+template <int DS>
+__device__ __forceinline__ void xcd_unit(unsigned b, std::size_t &unit, int &dq) {
+  const unsigned j = b >> 3;
+  unit = static_cast<std::size_t>(j / DS) * 8 + (b & 7);
+  dq = static_cast<int>(j % DS);
+}
+
+template <int DS> inline unsigned xcd_grid(std::size_t units) {
+  return static_cast<unsigned>(((units + 7) / 8) * 8 * DS);
+}
+
+} // namespace raftinfer::amd

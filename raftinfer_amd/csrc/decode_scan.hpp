@@ -221,6 +221,10 @@ __device__ __forceinline__ void combine_waves(const ScanShared<NH, WAVES> &sh, i
   a_out = a;
 }
 
-__device__ __forceinline__ float sigmoid_gate(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// sigmoid(x) = 1 / (1 + 2^(-x log2 e)) with the hardware exp2 and reciprocal
+// (about 1 ulp each; outputs are rounded to bf16 or compared at 1e-2).
+__device__ __forceinline__ float sigmoid_gate(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e));
+}
 
 } // namespace raftinfer::amd
