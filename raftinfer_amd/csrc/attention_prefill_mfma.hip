@@ -69,13 +69,12 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(
   // Q as the B operand: lane holds query `col`, dims kb*16 + half*8 .. +8.
   bf16x8 qb[16];
   {
-    const bool valid = static_cast<std::size_t>(col) < q_rows;
-    const bf16_bits *qrow = query + ((t0 + col) * kQueryHeads + head) * kHeadDim + half * 8;
+    // Query rows past the tile's end read the last row; they are never stored.
+    const std::size_t qr = static_cast<std::size_t>(col) < q_rows ? col : q_rows - 1;
+    const bf16_bits *qrow = query + ((t0 + qr) * kQueryHeads + head) * kHeadDim + half * 8;
 #pragma unroll
-    for (int kb = 0; kb < 16; ++kb) {
-      const u32x4 w = valid ? *reinterpret_cast<const u32x4 *>(qrow + kb * 16) : u32x4{0u, 0u, 0u, 0u};
-      qb[kb] = __builtin_bit_cast(bf16x8, w);
-    }
+    for (int kb = 0; kb < 16; ++kb)
+      qb[kb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(qrow + kb * 16));
   }
 
   floatx16 o[8];
@@ -92,15 +91,13 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(
   auto load_tile = [&](std::size_t k0) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const std::size_t key = k0 + 4 * kg + j;
-      if (key < key_end) {
-        const std::size_t row = cache_row(head_major, key, kv_head, max_ctx) + 8 * db;
-        kc[j] = *reinterpret_cast<const u32x4 *>(cache + row);
-        vc[j] = *reinterpret_cast<const u32x4 *>(cache + plane + row);
-      } else {
-        kc[j] = u32x4{0u, 0u, 0u, 0u};
-        vc[j] = u32x4{0u, 0u, 0u, 0u};
-      }
+      // Keys past key_end read row key_end-1 (in bounds); their scores are
+      // masked to -inf, so no branch splits the batch of loads.
+      std::size_t key = k0 + 4 * kg + j;
+      key = key < key_end ? key : key_end - 1;
+      const std::size_t row = cache_row(head_major, key, kv_head, max_ctx) + 8 * db;
+      kc[j] = *reinterpret_cast<const u32x4 *>(cache + row);
+      vc[j] = *reinterpret_cast<const u32x4 *>(cache + plane + row);
     }
   };
   load_tile(0);
@@ -193,8 +190,9 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb) {
     const std::size_t idx = base + nb * 32 + d0;
-    gv[nb][0] = row_ok ? *reinterpret_cast<const u32x4 *>(gate + idx) : u32x4{0u, 0u, 0u, 0u};
-    gv[nb][1] = row_ok ? *reinterpret_cast<const u32x4 *>(gate + idx + 8) : u32x4{0u, 0u, 0u, 0u};
+    const std::size_t gidx = row_ok ? idx : nb * 32 + d0 + ((t0 * kQueryHeads + head) * kHeadDim);
+    gv[nb][0] = *reinterpret_cast<const u32x4 *>(gate + gidx);
+    gv[nb][1] = *reinterpret_cast<const u32x4 *>(gate + gidx + 8);
   }
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb) {

@@ -119,24 +119,24 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
     u32x4 kv[2][8];
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
-      const std::size_t tok = c0 + 16 * g + n;
+      // Tokens past `end` read row end-1 (in bounds); their scores are masked.
+      std::size_t tok = c0 + 16 * g + n;
+      tok = tok < end ? tok : end - 1;
       const bf16_bits *row = tok == pos ? a.key_new + kv_head * kHeadDim
                                         : kplane + cache_row(a.head_major, tok, kv_head, a.max_ctx);
 #pragma unroll
       for (int kb = 0; kb < 8; ++kb)
-        kv[g][kb] = tok < end ? *reinterpret_cast<const u32x4 *>(row + kb * 32 + kq * 8)
-                              : u32x4{0u, 0u, 0u, 0u};
+        kv[g][kb] = *reinterpret_cast<const u32x4 *>(row + kb * 32 + kq * 8);
     }
     VRow<VEC> vv[TPL];
 #pragma unroll
     for (int j = 0; j < TPL; ++j) {
-      const std::size_t tok = c0 + tl + TL * j;
+      // Tokens past `end` read row end-1; their probability is zero.
+      std::size_t tok = c0 + tl + TL * j;
+      tok = tok < end ? tok : end - 1;
       const bf16_bits *row = tok == pos ? a.value_new + kv_head * kHeadDim
                                         : vplane + cache_row(a.head_major, tok, kv_head, a.max_ctx);
-      if (tok < end)
-        vv[j].load(row + dq * DIMS + VEC * dl);
-      else
-        vv[j].zero();
+      vv[j].load(row + dq * DIMS + VEC * dl);
     }
     // Scores: tile g holds S[token 16g + kq*4 + i][head n].
     floatx4 s[2];

@@ -24,6 +24,7 @@
 //   3. out_norm_kernel    RMSNorm(raw) * w * SiLU(z) -> activation dtype.
 // Host validation mirrors cpp/kernels/qwen35_delta.cu:26-135, :761-897.
 #include "common.hpp"
+#include "decode_scan.hpp"
 #include "raftinfer_amd/qwen35_delta.hpp"
 
 #include <cmath>
@@ -237,6 +238,112 @@ __global__ __launch_bounds__(256) void conv_norm_kernel(
   }
 }
 
+// Vector loads of 8 consecutive activation / weight values.
+template <typename T> __device__ __forceinline__ void load8(const T *p, float (&x)[8]) {
+  if constexpr (std::is_same_v<T, float>) {
+    const float4 a = *reinterpret_cast<const float4 *>(p), b = *reinterpret_cast<const float4 *>(p + 4);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+  } else {
+    const u32x4 w = *reinterpret_cast<const u32x4 *>(p);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const std::uint16_t bits = static_cast<std::uint16_t>(w[e >> 1] >> ((e & 1) * 16));
+      if constexpr (std::is_same_v<T, bf16_bits>)
+        x[e] = bf16_to_f32(bits);
+      else
+        x[e] = static_cast<float>(__builtin_bit_cast(_Float16, bits));
+    }
+  }
+}
+
+// Qwen3.5 head dims (dk = dv = 128): one block per token, 8 channels per
+// thread; a 128-channel head is one 16-lane DPP row, so the q/k L2 norms
+// reduce in-row.  Same math as conv_norm_kernel.
+template <typename T, typename Wt, int W>
+__global__ __launch_bounds__(256) void conv_norm_fast_kernel(
+    const T *__restrict__ input, const Wt *__restrict__ conv_w, const float *__restrict__ conv_state,
+    const Wt *__restrict__ recurrent_a, const Wt *__restrict__ dt_bias, float *__restrict__ convolved,
+    float *__restrict__ beta, float *__restrict__ gdecay, std::size_t stride, std::size_t conv_dim,
+    std::size_t qk_channels, std::size_t hv) {
+  constexpr int H = W - 1;
+  const std::size_t t = blockIdx.x;
+  const float qscale = 1.0f / sqrtf(static_cast<float>(kChunkDim));
+  for (std::size_t base = 0; base < conv_dim; base += 2048) {
+    const std::size_t c = base + 8 * threadIdx.x;
+    float cur[8], prev[H > 0 ? H : 1][8], w[8][W];
+    load8(input + t * stride + c, cur);
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      const std::size_t src = t + h;
+      if (src < static_cast<std::size_t>(H)) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) prev[h][e] = conv_state[(c + e) * H + src];
+      } else {
+        load8(input + (src - H) * stride + c, prev[h]);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int k = 0; k < W; ++k) w[e][k] = Elem<Wt>::load(conv_w, (c + e) * W + k);
+    float y[8], ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float sum = cur[e] * w[e][H];
+#pragma unroll
+      for (int h = 0; h < H; ++h) sum += prev[h][e] * w[e][h];
+      y[e] = silu(sum);
+      ss += y[e] * y[e];
+    }
+    if (c < qk_channels) { // q or k head: L2 norm over its 128 channels
+      ss = row16_sum(ss);
+      float scale = 1.0f / sqrtf(ss + kQkNormEpsilon);
+      if (c < qk_channels / 2) scale *= qscale;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] *= scale;
+    }
+    float *dst = convolved + t * conv_dim + c;
+    *reinterpret_cast<float4 *>(dst) = make_float4(y[0], y[1], y[2], y[3]);
+    *reinterpret_cast<float4 *>(dst + 4) = make_float4(y[4], y[5], y[6], y[7]);
+  }
+  for (std::size_t h = threadIdx.x; h < hv; h += 256) {
+    const float b = Elem<T>::load(input, t * stride + conv_dim + h);
+    const float a = Elem<T>::load(input, t * stride + conv_dim + hv + h);
+    beta[t * hv + h] = sigmoid(b);
+    gdecay[t * hv + h] = Elem<Wt>::load(recurrent_a, h) * softplus(a + Elem<Wt>::load(dt_bias, h));
+  }
+}
+
+// One block per token; a 128-wide value head is one 16-lane DPP row.
+template <typename T, typename Wt>
+__global__ __launch_bounds__(256) void out_norm_fast_kernel(const T *__restrict__ input,
+                                                            const Wt *__restrict__ norm_w,
+                                                            const float *__restrict__ raw,
+                                                            T *__restrict__ output,
+                                                            std::size_t stride, std::size_t conv_dim,
+                                                            std::size_t hv, float eps) {
+  const std::size_t t = blockIdx.x;
+  const std::size_t hidden = hv * kChunkDim;
+  for (std::size_t base = 0; base < hidden; base += 2048) {
+    const std::size_t c = base + 8 * threadIdx.x;
+    const float4 r0 = *reinterpret_cast<const float4 *>(raw + t * hidden + c);
+    const float4 r1 = *reinterpret_cast<const float4 *>(raw + t * hidden + c + 4);
+    const float x[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+    ss = row16_sum(ss);
+    const float scale = rsqrtf(ss / static_cast<float>(kChunkDim) + eps);
+    float z[8];
+    load8(input + t * stride + conv_dim + 2 * hv + c, z);
+    const std::size_t wc = c % kChunkDim;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      Elem<T>::store(output, t * hidden + c + e,
+                     x[e] * scale * Elem<Wt>::load(norm_w, wc + e) * silu(z[e]));
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void conv_state_kernel(const T *__restrict__ input,
                                                          float *__restrict__ conv_state,
@@ -335,6 +442,69 @@ struct ChunkScratch {
   float *g; // [hv][tokens] cumulative log decay within the chunk
 };
 
+// Batched staging of a 64 x 128 block of rows (rows >= L repeat row L-1): thread owns
+// rows (tid + 256 r) / 16, dims 8 * ((tid + 256 r) % 16), r = 0..3, so every
+// global load of the block is issued before any of them is consumed.
+template <typename T> struct RowBlock {
+  Chunk8<T> c[4];
+  template <typename Addr>
+  __device__ __forceinline__ void load(int L, Addr addr) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int p = threadIdx.x + 256 * r;
+      const int i = p >> 4, d = 8 * (p & 15);
+      // Rows past L load row L-1 (in bounds, finite); every consumer gives
+      // them zero weight, and no branch splits the batch of loads.
+      c[r].load(addr(i < L ? i : L - 1, d));
+    }
+  }
+  __device__ __forceinline__ void store(float (*dst)[kLd], float scale) const {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int p = threadIdx.x + 256 * r;
+      const int i = p >> 4, d = 8 * (p & 15);
+      float4 lo, hi;
+      lo.x = c[r].get(0) * scale; lo.y = c[r].get(1) * scale; lo.z = c[r].get(2) * scale; lo.w = c[r].get(3) * scale;
+      hi.x = c[r].get(4) * scale; hi.y = c[r].get(5) * scale; hi.z = c[r].get(6) * scale; hi.w = c[r].get(7) * scale;
+      *reinterpret_cast<float4 *>(&dst[i][d]) = lo;
+      *reinterpret_cast<float4 *>(&dst[i][d + 4]) = hi;
+    }
+  }
+};
+
+template <> struct RowBlock<float> {
+  float4 c[4][2];
+  template <typename Addr>
+  __device__ __forceinline__ void load(int L, Addr addr) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int p = threadIdx.x + 256 * r;
+      const int i = p >> 4, d = 8 * (p & 15);
+      const float *src = addr(i < L ? i : L - 1, d);
+      c[r][0] = *reinterpret_cast<const float4 *>(src);
+      c[r][1] = *reinterpret_cast<const float4 *>(src + 4);
+    }
+  }
+  __device__ __forceinline__ void store(float (*dst)[kLd], float scale) const {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int p = threadIdx.x + 256 * r;
+      const int i = p >> 4, d = 8 * (p & 15);
+#pragma unroll
+      for (int hpart = 0; hpart < 2; ++hpart) {
+        float4 v = c[r][hpart];
+        v.x *= scale; v.y *= scale; v.z *= scale; v.w *= scale;
+        *reinterpret_cast<float4 *>(&dst[i][d + 4 * hpart]) = v;
+      }
+    }
+  }
+};
+
+template <typename T>
+__device__ __forceinline__ const T *src_row(const Src<T> &s, std::size_t t, std::size_t head, int d) {
+  return s.base + t * s.row + head * s.head_stride + d;
+}
+
 struct PrepShared {
   float k[kChunk][kLd];
   float qv[kChunk][kLd];
@@ -358,15 +528,21 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
   const std::size_t t0 = static_cast<std::size_t>(blockIdx.y) * kChunk;
   const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
 
-  for (int e = tid; e < kChunk * kChunkDim; e += 256) {
-    const int i = e / kChunkDim, d = e % kChunkDim;
-    const bool ok = i < L;
-    sh.k[i][d] = ok ? ks.at(t0 + i, kh, d) : 0.f;
-    sh.qv[i][d] = ok ? qs.at(t0 + i, kh, d) : 0.f;
+  RowBlock<InT> kb, qb;
+  kb.load(L, [&](int i, int d) { return src_row(ks, t0 + i, kh, d); });
+  qb.load(L, [&](int i, int d) { return src_row(qs, t0 + i, kh, d); });
+  float bt = 0.f, gt = 0.f;
+  if (tid < L) {
+    bt = beta[(t0 + tid) * hv + h];
+    gt = gdecay[(t0 + tid) * hv + h];
   }
+  kb.store(sh.k, ks.scale);
+  qb.store(sh.qv, qs.scale);
+  RowBlock<InT> vb; // issued now, consumed after the Q-dependent products
+  vb.load(L, [&](int i, int d) { return src_row(vs, t0 + i, h, d); });
   if (tid < kChunk) {
-    sh.beta[tid] = tid < L ? beta[(t0 + tid) * hv + h] : 0.f;
-    sh.g[tid] = tid < L ? gdecay[(t0 + tid) * hv + h] : 0.f;
+    sh.beta[tid] = bt;
+    sh.g[tid] = gt;
   }
   __syncthreads();
   if (tid == 0) {
@@ -382,6 +558,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
   for (int tj = 0; tj < 4; ++tj) {
     floatx4 acc = floatx4{};
     if (tj <= wave) {
+#pragma unroll 8
       for (int k0 = 0; k0 < kChunkDim; k0 += 4)
         acc = mfma4(sh.qv[wave * 16 + lr][k0 + lk], sh.k[tj * 16 + lr][k0 + lk], acc);
     }
@@ -396,6 +573,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
   for (int tj = 0; tj < 4; ++tj) {
     floatx4 acc = floatx4{};
     if (tj <= wave) {
+#pragma unroll 8
       for (int k0 = 0; k0 < kChunkDim; k0 += 4)
         acc = mfma4(sh.k[wave * 16 + lr][k0 + lk], sh.k[tj * 16 + lr][k0 + lk], acc);
     }
@@ -406,28 +584,42 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
     }
   }
   __syncthreads();
-  // Q no longer needed: stage V.
-  for (int e = tid; e < kChunk * kChunkDim; e += 256) {
-    const int i = e / kChunkDim, d = e % kChunkDim;
-    sh.qv[i][d] = i < L ? vs.at(t0 + i, h, d) : 0.f;
-  }
-  // T = (I + A)^-1 by forward substitution, lane = column (wave 0).
-  if (wave == 0) {
-    float col[kChunk];
+  vb.store(sh.qv, vs.scale); // Q no longer needed: stage V.
+  // T = (I + A)^-1 (A strictly lower) in 16-row blocks: for block ib,
+  // rhs = E - A[rows, 0:16ib] T[0:16ib, :] on MFMA (wave = 16-column tile),
+  // then rows r of the block: T_r = rhs_r - sum_{16ib<=j<r} A_rj T_j (wave 0,
+  // lane = column).
+  for (int ib = 0; ib < 4; ++ib) {
+    {
+      floatx4 acc = floatx4{};
+      const int cb = wave * 16;
+      for (int k0 = 0; k0 < 16 * ib; k0 += 4)
+        acc = mfma4(sh.a[16 * ib + lr][k0 + lk], sh.tm[k0 + lk][cb + lr], acc);
 #pragma unroll
-    for (int i = 0; i < kChunk; ++i) {
-      float acc = i == lane ? 1.f : 0.f;
-#pragma unroll
-      for (int j = 0; j < i; ++j) acc = fmaf(-sh.a[i][j], col[j], acc);
-      col[i] = acc;
-      sh.tm[i][lane] = acc;
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * ib + lk * 4 + r, c = cb + lr;
+        sh.tm[row][c] = (row == c ? 1.f : 0.f) - acc[r];
+      }
     }
+    __syncthreads();
+    if (wave == 0) {
+      float x[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float v = sh.tm[16 * ib + r][lane];
+#pragma unroll
+        for (int j = 0; j < r; ++j) v = fmaf(-sh.a[16 * ib + r][16 * ib + j], x[j], v);
+        x[r] = v;
+        sh.tm[16 * ib + r][lane] = v;
+      }
+    }
+    __syncthreads();
   }
-  __syncthreads();
   // W = T diag(beta e^G) K, U = T diag(beta) V: 4 x 8 output tiles.
   for (int tile = wave; tile < 32; tile += 4) {
     const int ti = tile >> 3, tn = tile & 7;
     floatx4 aw = floatx4{}, au = floatx4{};
+#pragma unroll 4
     for (int j0 = 0; j0 < kChunk; j0 += 4) {
       const int j = j0 + lk;
       const float tmv = sh.tm[ti * 16 + lr][j];
@@ -448,13 +640,57 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
 }
 
 struct ScanShared {
-  float wq[kChunk][kLd]; // W, then Q
+  float w[kChunk][kLd];
+  float q[kChunk][kLd];
   float k[kChunk][kLd];
   float s[kChunkDim][kLdB];
   float d[kChunk][kLdB];
   float u[kChunk][kLdB];
   float m[kChunk][kLdC];
   float g[kChunk];
+};
+
+// All global inputs of one chunk, held in registers so the next chunk's loads
+// are in flight while the current chunk is computed.
+template <typename InT> struct ScanChunk {
+  RowBlock<float> w;
+  RowBlock<InT> q, k;
+  float4 m[4];
+  float4 u;
+  float g;
+  __device__ __forceinline__ void load(const Src<InT> &qs, const Src<InT> &ks,
+                                       const ChunkScratch &sc, std::size_t h, std::size_t kh,
+                                       std::size_t tokens, std::size_t t0, int c0) {
+    const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
+    const int tid = threadIdx.x;
+    w.load(L, [&](int i, int d) { return sc.w + (h * tokens + t0 + i) * kChunkDim + d; });
+    q.load(L, [&](int i, int d) { return src_row(qs, t0 + i, kh, d); });
+    k.load(L, [&](int i, int d) { return src_row(ks, t0 + i, kh, d); });
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int p = tid + 256 * r;
+      const int i = p >> 4, j = 4 * (p & 15);
+      m[r] = *reinterpret_cast<const float4 *>(sc.m + (h * tokens + t0 + (i < L ? i : L - 1)) * kChunk + j);
+    }
+    {
+      const int i = tid >> 2, c = 4 * (tid & 3);
+      u = *reinterpret_cast<const float4 *>(sc.u + (h * tokens + t0 + (i < L ? i : L - 1)) * kChunkDim + c0 + c);
+    }
+    g = sc.g[h * tokens + t0 + (tid < L ? tid : L - 1)];
+  }
+  __device__ __forceinline__ void store(ScanShared &sh, float qscale, float kscale) const {
+    const int tid = threadIdx.x;
+    w.store(sh.w, 1.0f);
+    q.store(sh.q, qscale);
+    k.store(sh.k, kscale);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int p = tid + 256 * r;
+      *reinterpret_cast<float4 *>(&sh.m[p >> 4][4 * (p & 15)]) = m[r];
+    }
+    *reinterpret_cast<float4 *>(&sh.u[tid >> 2][4 * (tid & 3)]) = u;
+    if (tid < kChunk) sh.g[tid] = g;
+  }
 };
 
 // Block (value head, 16-column block), sequential over chunks.
@@ -471,6 +707,8 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(Src<InT> qs, Src<InT> k
   const std::size_t kh = h % hk;
   const int c0 = blockIdx.y * kColBlock;
   float *sg = state + h * kChunkDim * kChunkDim;
+  ScanChunk<InT> regs;
+  regs.load(qs, ks, scratch, h, kh, tokens, 0, c0);
   for (int e = tid; e < kChunkDim * kColBlock; e += 256) {
     const int r = e / kColBlock, c = e % kColBlock;
     sh.s[r][c] = sg[r * kChunkDim + c0 + c];
@@ -478,27 +716,15 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(Src<InT> qs, Src<InT> k
   for (std::size_t t0 = 0; t0 < tokens; t0 += kChunk) {
     const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
     __syncthreads();
-    for (int e = tid; e < kChunk * kChunkDim; e += 256) {
-      const int i = e / kChunkDim, d = e % kChunkDim;
-      const bool ok = i < L;
-      sh.wq[i][d] = ok ? scratch.w[(h * tokens + t0 + i) * kChunkDim + d] : 0.f;
-      sh.k[i][d] = ok ? ks.at(t0 + i, kh, d) : 0.f;
-    }
-    for (int e = tid; e < kChunk * kChunk; e += 256) {
-      const int i = e / kChunk, j = e % kChunk;
-      sh.m[i][j] = i < L ? scratch.m[(h * tokens + t0 + i) * kChunk + j] : 0.f;
-    }
-    for (int e = tid; e < kChunk * kColBlock; e += 256) {
-      const int i = e / kColBlock, c = e % kColBlock;
-      sh.u[i][c] = i < L ? scratch.u[(h * tokens + t0 + i) * kChunkDim + c0 + c] : 0.f;
-    }
-    if (tid < kChunk) sh.g[tid] = tid < L ? scratch.g[h * tokens + t0 + tid] : 0.f;
+    regs.store(sh, qs.scale, ks.scale);
     __syncthreads();
+    if (t0 + kChunk < tokens) regs.load(qs, ks, scratch, h, kh, tokens, t0 + kChunk, c0);
     // D = U - W S (row tile = wave).
     {
       floatx4 acc = floatx4{};
+#pragma unroll 8
       for (int k0 = 0; k0 < kChunkDim; k0 += 4)
-        acc = mfma4(sh.wq[wave * 16 + lr][k0 + lk], sh.s[k0 + lk][lr], acc);
+        acc = mfma4(sh.w[wave * 16 + lr][k0 + lk], sh.s[k0 + lk][lr], acc);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = wave * 16 + lk * 4 + r;
@@ -506,16 +732,13 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(Src<InT> qs, Src<InT> k
       }
     }
     __syncthreads();
-    for (int e = tid; e < kChunk * kChunkDim; e += 256) {
-      const int i = e / kChunkDim, d = e % kChunkDim;
-      sh.wq[i][d] = i < L ? qs.at(t0 + i, kh, d) : 0.f;
-    }
-    __syncthreads();
     // O = e^G (Q S) + M D.
     {
       floatx4 qsacc = floatx4{}, md = floatx4{};
+#pragma unroll 8
       for (int k0 = 0; k0 < kChunkDim; k0 += 4)
-        qsacc = mfma4(sh.wq[wave * 16 + lr][k0 + lk], sh.s[k0 + lk][lr], qsacc);
+        qsacc = mfma4(sh.q[wave * 16 + lr][k0 + lk], sh.s[k0 + lk][lr], qsacc);
+#pragma unroll 4
       for (int j0 = 0; j0 < kChunk; j0 += 4)
         md = mfma4(sh.m[wave * 16 + lr][j0 + lk], sh.d[j0 + lk][lr], md);
 #pragma unroll
@@ -533,6 +756,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(Src<InT> qs, Src<InT> k
     for (int tt = 0; tt < 2; ++tt) {
       const int rt = 2 * wave + tt;
       floatx4 acc = floatx4{};
+#pragma unroll 4
       for (int j0 = 0; j0 < kChunk; j0 += 4) {
         const int j = j0 + lk;
         const float a = j < L ? sh.k[j][rt * 16 + lr] * __expf(glast - sh.g[j]) : 0.f;
@@ -632,11 +856,23 @@ void launch_typed(const void *input, const void *conv_weight, const void *recurr
   scratch.m = scratch.u + s.value_heads * s.tokens * s.value_dim;
   scratch.g = scratch.m + s.value_heads * s.tokens * kChunk;
 
-  const dim3 cgrid{static_cast<unsigned>(s.tokens), static_cast<unsigned>(2 * s.key_heads + s.value_heads), 1};
-  conv_norm_kernel<T, Wt><<<cgrid, 256, 0, stream>>>(
-      in, static_cast<const Wt *>(conv_weight), conv_state, static_cast<const Wt *>(recurrent_a),
-      static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, s.tokens, c.token_stride, c.conv_dim,
-      s.key_heads, s.value_heads, s.key_dim, s.value_dim, s.conv_width);
+  const bool fast = s.key_dim == kChunkDim && s.value_dim == kChunkDim && s.conv_width == 4 &&
+                    c.conv_dim % 2048 == 0 && s.hidden_size % 2048 == 0 &&
+                    c.token_stride % 8 == 0 &&
+                    (reinterpret_cast<std::uintptr_t>(input) & 15u) == 0 &&
+                    (reinterpret_cast<std::uintptr_t>(ws) & 15u) == 0;
+  if (fast) {
+    conv_norm_fast_kernel<T, Wt, 4><<<static_cast<unsigned>(s.tokens), 256, 0, stream>>>(
+        in, static_cast<const Wt *>(conv_weight), conv_state, static_cast<const Wt *>(recurrent_a),
+        static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, c.token_stride, c.conv_dim,
+        2 * c.key_size, s.value_heads);
+  } else {
+    const dim3 cgrid{static_cast<unsigned>(s.tokens), static_cast<unsigned>(2 * s.key_heads + s.value_heads), 1};
+    conv_norm_kernel<T, Wt><<<cgrid, 256, 0, stream>>>(
+        in, static_cast<const Wt *>(conv_weight), conv_state, static_cast<const Wt *>(recurrent_a),
+        static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, s.tokens, c.token_stride, c.conv_dim,
+        s.key_heads, s.value_heads, s.key_dim, s.value_dim, s.conv_width);
+  }
   check_launch<Err>("qwen35_gated_delta batched convolution");
   if (s.conv_width > 1) {
     conv_state_kernel<T><<<static_cast<unsigned>(ceil_div_unchecked(c.conv_dim, 256)), 256, 0, stream>>>(
@@ -648,10 +884,17 @@ void launch_typed(const void *input, const void *conv_weight, const void *recurr
   const Src<float> v{convolved + 2 * c.key_size, c.conv_dim, s.value_dim, 1.0f};
   launch_recurrence<float, float>(q, k, v, beta, gdecay, rec_state, raw, scratch, s.tokens,
                                   s.key_heads, s.value_heads, s.key_dim, s.value_dim,
-                                  use_chunked(s, policy), stream);
-  out_norm_kernel<T, Wt><<<static_cast<unsigned>(s.tokens * s.value_heads), 256, 0, stream>>>(
-      in, static_cast<const Wt *>(norm_w), raw, static_cast<T *>(output), c.token_stride, c.conv_dim,
-      s.value_heads, s.value_dim, s.epsilon);
+                                  use_chunked(s, policy) &&
+                                      (reinterpret_cast<std::uintptr_t>(ws) & 15u) == 0,
+                                  stream);
+  if (fast)
+    out_norm_fast_kernel<T, Wt><<<static_cast<unsigned>(s.tokens), 256, 0, stream>>>(
+        in, static_cast<const Wt *>(norm_w), raw, static_cast<T *>(output), c.token_stride,
+        c.conv_dim, s.value_heads, s.epsilon);
+  else
+    out_norm_kernel<T, Wt><<<static_cast<unsigned>(s.tokens * s.value_heads), 256, 0, stream>>>(
+        in, static_cast<const Wt *>(norm_w), raw, static_cast<T *>(output), c.token_stride, c.conv_dim,
+        s.value_heads, s.value_dim, s.epsilon);
   check_launch<Err>("qwen35_gated_delta batched output normalization");
 }
 
@@ -788,6 +1031,10 @@ void qwen35_gated_delta_core(const void *q, const void *k, const void *v, const 
   if (chunked) {
     require<Err>(s.key_dim == kChunkDim && s.value_dim == kChunkDim,
                  "chunked gated-delta requires key_dim = value_dim = 128");
+    require<Err>(((reinterpret_cast<std::uintptr_t>(q) | reinterpret_cast<std::uintptr_t>(k) |
+                   reinterpret_cast<std::uintptr_t>(v) | reinterpret_cast<std::uintptr_t>(workspace)) &
+                  15u) == 0,
+                 "chunked gated-delta needs 16-byte aligned q, k, v and workspace");
     require<Err>(workspace != nullptr && workspace_bytes >= qwen35_gated_delta_core_workspace_bytes(s),
                  "gated-delta core workspace is too small");
   }
