@@ -433,7 +433,6 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
 
 constexpr int kLd = kChunkDim + 4; // LDS row stride for 128-wide rows
 constexpr int kLdC = kChunk + 4;   // LDS row stride for 64-wide rows
-constexpr int kLdB = kColBlock + 4;
 
 struct ChunkScratch {
   float *w; // [hv][tokens][dk]
@@ -639,16 +638,30 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
   if (tid < L) scratch.g[h * tokens + t0 + tid] = sh.g[tid];
 }
 
+// LDS of the chunk scan.  Every MFMA operand is read as a float4 along its
+// contraction index: lane group lk = lane/16 supplies indices 4*lk .. 4*lk+3 of
+// each 16-wide slice to four consecutive MFMAs (mfma4x4), which together sum
+// over the whole slice.
 struct ScanShared {
-  float w[kChunk][kLd];
-  float q[kChunk][kLd];
-  float k[kChunk][kLd];
-  float s[kChunkDim][kLdB];
-  float d[kChunk][kLdB];
-  float u[kChunk][kLdB];
-  float m[kChunk][kLdC];
+  float w[kChunk][kLd];      // W rows
+  float q[kChunk][kLd];      // Q rows x q scale
+  float k[kChunk][kLd];      // K rows x k scale
+  float st[kColBlock][kLd];  // S^T: [state column][key dim]
+  float dt[kColBlock][kLdC]; // D^T: [state column][token]
+  float m[kChunk][kLdC];     // M rows
   float g[kChunk];
+  float f[kChunk];           // e^{G_last - G_j}; 0 past the chunk end
+  float eg[kChunk];          // e^{G_i}
 };
+
+__device__ __forceinline__ float4 lds4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+
+__device__ __forceinline__ floatx4 mfma4x4(float4 a, float4 b, floatx4 c) {
+  c = mfma4(a.x, b.x, c);
+  c = mfma4(a.y, b.y, c);
+  c = mfma4(a.z, b.z, c);
+  return mfma4(a.w, b.w, c);
+}
 
 // All global inputs of one chunk, held in registers so the next chunk's loads
 // are in flight while the current chunk is computed.
@@ -656,13 +669,13 @@ template <typename InT> struct ScanChunk {
   RowBlock<float> w;
   RowBlock<InT> q, k;
   float4 m[4];
-  float4 u;
+  floatx4 u; // U[wave*16 + lk*4 + r][c0 + lr]
   float g;
   __device__ __forceinline__ void load(const Src<InT> &qs, const Src<InT> &ks,
                                        const ChunkScratch &sc, std::size_t h, std::size_t kh,
                                        std::size_t tokens, std::size_t t0, int c0) {
     const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     w.load(L, [&](int i, int d) { return sc.w + (h * tokens + t0 + i) * kChunkDim + d; });
     q.load(L, [&](int i, int d) { return src_row(qs, t0 + i, kh, d); });
     k.load(L, [&](int i, int d) { return src_row(ks, t0 + i, kh, d); });
@@ -672,9 +685,10 @@ template <typename InT> struct ScanChunk {
       const int i = p >> 4, j = 4 * (p & 15);
       m[r] = *reinterpret_cast<const float4 *>(sc.m + (h * tokens + t0 + (i < L ? i : L - 1)) * kChunk + j);
     }
-    {
-      const int i = tid >> 2, c = 4 * (tid & 3);
-      u = *reinterpret_cast<const float4 *>(sc.u + (h * tokens + t0 + (i < L ? i : L - 1)) * kChunkDim + c0 + c);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = wave * 16 + (lane >> 4) * 4 + r;
+      u[r] = sc.u[(h * tokens + t0 + (i < L ? i : L - 1)) * kChunkDim + c0 + (lane & 15)];
     }
     g = sc.g[h * tokens + t0 + (tid < L ? tid : L - 1)];
   }
@@ -688,12 +702,12 @@ template <typename InT> struct ScanChunk {
       const int p = tid + 256 * r;
       *reinterpret_cast<float4 *>(&sh.m[p >> 4][4 * (p & 15)]) = m[r];
     }
-    *reinterpret_cast<float4 *>(&sh.u[tid >> 2][4 * (tid & 3)]) = u;
     if (tid < kChunk) sh.g[tid] = g;
   }
 };
 
-// Block (value head, 16-column block), sequential over chunks.
+// Block (value head, 16-column block), sequential over chunks.  Wave w owns
+// rows 16w.. of D and O and state rows 32w.. of the S update.
 template <typename InT, typename OutT>
 __global__ __launch_bounds__(256) void chunk_scan_kernel(Src<InT> qs, Src<InT> ks,
                                                          ChunkScratch scratch,
@@ -711,72 +725,91 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(Src<InT> qs, Src<InT> k
   regs.load(qs, ks, scratch, h, kh, tokens, 0, c0);
   for (int e = tid; e < kChunkDim * kColBlock; e += 256) {
     const int r = e / kColBlock, c = e % kColBlock;
-    sh.s[r][c] = sg[r * kChunkDim + c0 + c];
+    sh.st[c][r] = sg[r * kChunkDim + c0 + c];
   }
   for (std::size_t t0 = 0; t0 < tokens; t0 += kChunk) {
     const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
     __syncthreads();
     regs.store(sh, qs.scale, ks.scale);
+    const floatx4 u = regs.u;
     __syncthreads();
     if (t0 + kChunk < tokens) regs.load(qs, ks, scratch, h, kh, tokens, t0 + kChunk, c0);
-    // D = U - W S (row tile = wave).
+    if (tid < kChunk) {
+      const float gi = sh.g[tid];
+      sh.f[tid] = tid < L ? __expf(sh.g[L - 1] - gi) : 0.f;
+      sh.eg[tid] = __expf(gi);
+    }
+    // D = U - W S.
     {
-      floatx4 acc = floatx4{};
-#pragma unroll 8
-      for (int k0 = 0; k0 < kChunkDim; k0 += 4)
-        acc = mfma4(sh.w[wave * 16 + lr][k0 + lk], sh.s[k0 + lk][lr], acc);
+      floatx4 a0 = floatx4{}, a1 = floatx4{};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = wave * 16 + lk * 4 + r;
-        sh.d[i][lr] = i < L ? sh.u[i][lr] - acc[r] : 0.f;
+      for (int kk = 0; kk < kChunkDim; kk += 32) {
+        a0 = mfma4x4(lds4(&sh.w[wave * 16 + lr][kk + 4 * lk]), lds4(&sh.st[lr][kk + 4 * lk]), a0);
+        a1 = mfma4x4(lds4(&sh.w[wave * 16 + lr][kk + 16 + 4 * lk]),
+                     lds4(&sh.st[lr][kk + 16 + 4 * lk]), a1);
       }
+      float4 dv;
+      dv.x = u[0] - (a0[0] + a1[0]);
+      dv.y = u[1] - (a0[1] + a1[1]);
+      dv.z = u[2] - (a0[2] + a1[2]);
+      dv.w = u[3] - (a0[3] + a1[3]);
+      *reinterpret_cast<float4 *>(&sh.dt[lr][wave * 16 + lk * 4]) = dv;
     }
     __syncthreads();
     // O = e^G (Q S) + M D.
     {
-      floatx4 qsacc = floatx4{}, md = floatx4{};
-#pragma unroll 8
-      for (int k0 = 0; k0 < kChunkDim; k0 += 4)
-        qsacc = mfma4(sh.q[wave * 16 + lr][k0 + lk], sh.s[k0 + lk][lr], qsacc);
-#pragma unroll 4
-      for (int j0 = 0; j0 < kChunk; j0 += 4)
-        md = mfma4(sh.m[wave * 16 + lr][j0 + lk], sh.d[j0 + lk][lr], md);
+      floatx4 qa = floatx4{}, ma = floatx4{};
+#pragma unroll
+      for (int kk = 0; kk < kChunkDim; kk += 16) {
+        qa = mfma4x4(lds4(&sh.q[wave * 16 + lr][kk + 4 * lk]), lds4(&sh.st[lr][kk + 4 * lk]), qa);
+        if (kk < kChunk)
+          ma = mfma4x4(lds4(&sh.m[wave * 16 + lr][kk + 4 * lk]), lds4(&sh.dt[lr][kk + 4 * lk]), ma);
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = wave * 16 + lk * 4 + r;
         if (i < L)
           Elem<OutT>::store(out, ((t0 + i) * hv + h) * kChunkDim + c0 + lr,
-                            __expf(sh.g[i]) * qsacc[r] + md[r]);
+                            fmaf(sh.eg[i], qa[r], ma[r]));
       }
     }
-    // S' = e^{G_last} S + (e^{G_last - G_j} K_j)^T D: row tiles 2*wave, 2*wave+1.
-    const float glast = sh.g[L - 1];
-    floatx4 snew[2];
+    // S'[d][c] = e^{G_last} S[d][c] + sum_j K[j][d] e^{G_last - G_j} D[j][c].
+    const float egl = sh.eg[L - 1];
+    floatx4 sn[2];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      const int rt = 2 * wave + tt;
+      const int d0 = (2 * wave + tt) * 16;
       floatx4 acc = floatx4{};
-#pragma unroll 4
-      for (int j0 = 0; j0 < kChunk; j0 += 4) {
-        const int j = j0 + lk;
-        const float a = j < L ? sh.k[j][rt * 16 + lr] * __expf(glast - sh.g[j]) : 0.f;
-        acc = mfma4(a, sh.d[j][lr], acc);
-      }
-      const float gl = __expf(glast);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = fmaf(gl, sh.s[rt * 16 + lk * 4 + r][lr], acc[r]);
-      snew[tt] = acc;
+      for (int jj = 0; jj < kChunk; jj += 16) {
+        const int j = jj + 4 * lk;
+        const float4 fv = lds4(&sh.f[j]);
+        float4 a;
+        a.x = sh.k[j][d0 + lr] * fv.x;
+        a.y = sh.k[j + 1][d0 + lr] * fv.y;
+        a.z = sh.k[j + 2][d0 + lr] * fv.z;
+        a.w = sh.k[j + 3][d0 + lr] * fv.w;
+        acc = mfma4x4(a, lds4(&sh.dt[lr][j]), acc);
+      }
+      const float4 so = lds4(&sh.st[lr][d0 + lk * 4]);
+      acc[0] = fmaf(egl, so.x, acc[0]);
+      acc[1] = fmaf(egl, so.y, acc[1]);
+      acc[2] = fmaf(egl, so.z, acc[2]);
+      acc[3] = fmaf(egl, so.w, acc[3]);
+      sn[tt] = acc;
     }
     __syncthreads();
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sh.s[(2 * wave + tt) * 16 + lk * 4 + r][lr] = snew[tt][r];
+    for (int tt = 0; tt < 2; ++tt) {
+      float4 v;
+      v.x = sn[tt][0]; v.y = sn[tt][1]; v.z = sn[tt][2]; v.w = sn[tt][3];
+      *reinterpret_cast<float4 *>(&sh.st[lr][(2 * wave + tt) * 16 + lk * 4]) = v;
+    }
   }
   __syncthreads();
   for (int e = tid; e < kChunkDim * kColBlock; e += 256) {
     const int r = e / kColBlock, c = e % kColBlock;
-    sg[r * kChunkDim + c0 + c] = sh.s[r][c];
+    sg[r * kChunkDim + c0 + c] = sh.st[c][r];
   }
 }
 
