@@ -96,6 +96,7 @@ constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141; // row_half_mirror
 constexpr int kDppMirror = 0x140;     // row_mirror
+constexpr int kDppRor12 = 0x12C;      // row_ror:12 (lane i reads lane (i + 4) % 16 of its row)
 
 __device__ __forceinline__ float row16_sum(float x) {
   x += dpp<kDppXor1>(x);
@@ -120,6 +121,25 @@ __device__ __forceinline__ float xor32(float x) {
   return __builtin_bit_cast(
       float, __builtin_amdgcn_ds_bpermute(((threadIdx.x ^ 32) & 63) << 2, __builtin_bit_cast(int, x)));
 }
+// Reduce-scatter step over lane halves / row pairs without the LDS crossbar.
+// v_permlane32_swap exchanges the upper 32 lanes of `a` with the lower 32 of
+// `b`; summing the two registers after it gives lanes 0..31 a[l] + a[l^32]
+// and lanes 32..63 b[l] + b[l^32].  v_permlane16_swap does the same for
+// odd/even 16-lane rows: even rows get a[l] + a[l^16], odd rows b[l] + b[l^16].
+// Written as inline asm: the compiler builtin's two results are folded into
+// one when both are used in the same expression.  The s_nop covers the
+// VALU-write -> permlane-read hazard of the operands.
+__device__ __forceinline__ float swap_sum32(float a, float b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return a + b;
+}
+__device__ __forceinline__ float swap_sum16(float a, float b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return a + b;
+}
+// x + x[lane ^ 8] (row_ror:8 reads lane ^ 8 of the row).
+__device__ __forceinline__ float sum_xor8(float x) { return x + dpp<0x128>(x); }
+
 __device__ __forceinline__ float wave_sum(float x) {
   x = row16_sum(x);
   x += xor16(x);
@@ -131,6 +151,13 @@ __device__ __forceinline__ float wave_max(float x) {
   x = fmaxf(x, xor16(x));
   x = fmaxf(x, xor32(x));
   return x;
+}
+
+// c + a.lo * b.lo + a.hi * b.hi for packed bf16 pairs (v_dot2_f32_bf16).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot2_bf16(std::uint32_t a, std::uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b),
+                                         c, false);
 }
 
 // Orders a wave's own LDS writes before its later LDS reads by other lanes.

@@ -12,9 +12,9 @@
 // its L2 (workgroups are dispatched round-robin over the 8 XCDs).
 //
 // Per wave, tokens are consumed 32 at a time:
-//   S[token][head] = v_mfma_f32_16x16x32_bf16(A = K rows, B = q^T) x 8 per 16 tokens
+//   S[token][head] = v_mfma_f32_16x16x32_bf16 on whole-line K loads
 //   online softmax in the exp2 domain (log2(e)/16 folded into the scale)
-//   O[head][dims] += p * V  on VALU (lane = dim pair x token phase)
+//   O[head][dims] += p * V  on VALU (lane = 16-byte V segment x token phase)
 #pragma once
 
 #include "decode_scan.hpp"
@@ -43,11 +43,11 @@ template <int DS, int WAVES> struct DecodeMfmaShared {
 // PV lane mapping for a DIMS-wide slice: a lane owns VEC consecutive dims
 // (one 2*VEC-byte load per token) and one of TL token phases.
 template <int DIMS> struct PvMap {
-  static constexpr int VEC = DIMS / 32 > 2 ? (DIMS / 32 > 8 ? 8 : DIMS / 32) : 2;
+  static constexpr int VEC = DIMS / 8 > 8 ? 8 : DIMS / 8;
   static constexpr int DL = DIMS / VEC;
   static constexpr int TL = 64 / DL;
   static constexpr int TPL = 32 / TL;
-  static_assert(DL * VEC == DIMS && DL * TL == 64 && TPL * TL == 32, "bad PV map");
+  static_assert(DL * VEC == DIMS && DL * TL == 64 && TPL * TL == 32 && DL >= 8, "bad PV map");
 };
 
 template <int VEC> struct VRow {
@@ -77,6 +77,17 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // Scans tokens [begin, end) of kv_head for the dims slice dq; leaves
 // per-wave (m, l, acc) in sh.  Row `pos` (the token being appended) is read
 // from key_new / value_new instead of the cache.
+//
+// Scores: a group of 8 tokens is read with 8 lanes per 128-byte line (4 loads
+// cover the 512-byte rows), so every load instruction fetches 8 whole lines,
+// and goes straight into v_mfma_f32_16x16x32_bf16 as the A operand: lane l
+// holds 16 bytes of token t = (l%16)/2 at segment 2*(l/16) + l%2 of the line,
+// i.e. A row m = 2t + half (half = l%2) with k = (l/16)*8 + j.  The B operand
+// holds, in column n = 4*half' + h (n < 8), head h's q at the same segments
+// for half' (columns 8..15 are zero), so C[2t + half][4*half + h] is the dot
+// over half of the line and the score is C[2t][h] + C[2t+1][4+h], two values
+// 4 lanes apart in a row (one DPP add).  After it, lane l with l%16 < 4 holds
+// head l%16's scores of tokens 2*(l/16) and 2*(l/16)+1 of the group.
 template <int DS, int WAVES>
 __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::size_t kv_head,
                                                  int dq, std::size_t begin, std::size_t end,
@@ -86,8 +97,11 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
   constexpr int VEC = Map::VEC, DL = Map::DL, TL = Map::TL, TPL = Map::TPL;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int n = lane & 15;  // head column of the score tile
-  const int kq = lane >> 4; // k-quarter of the MFMA operands
+  const int n = lane & 15;              // MFMA column (B / C) and row (A)
+  const int kq = lane >> 4;             // k-quarter (A / B), row quarter (C)
+  const int seg = 2 * kq + (lane & 1);  // 16-byte segment of the line this lane loads
+  const int rt = n >> 1;                // token of the group this lane loads
+  const bool head_lane = n < kGroup;    // lane holds scores of head n
   const int dl = lane % DL;
   const int tl = lane / DL;
   const float scale = kLog2e / 16.0f;
@@ -95,17 +109,18 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
   const bf16_bits *kplane = a.cache;
   const bf16_bits *vplane = a.cache + plane;
 
-  // q^T as the B operand: lane holds head n, dims kb*32 + kq*8 .. +8.
-  bf16x8 qb[8];
+  // B operand per line: column n < 8 = (half' = n/4, head n%4).
+  bf16x8 qb[4];
 #pragma unroll
-  for (int kb = 0; kb < 8; ++kb) {
+  for (int line = 0; line < 4; ++line) {
     u32x4 w = u32x4{0u, 0u, 0u, 0u};
-    if (n < kGroup)
-      w = *reinterpret_cast<const u32x4 *>(a.query + (kv_head * kGroup + n) * kHeadDim + kb * 32 + kq * 8);
-    qb[kb] = __builtin_bit_cast(bf16x8, w);
+    if (n < 8)
+      w = *reinterpret_cast<const u32x4 *>(a.query + (kv_head * kGroup + (n & 3)) * kHeadDim + line * 64 +
+                                           (2 * kq + (n >> 2)) * 8);
+    qb[line] = __builtin_bit_cast(bf16x8, w);
   }
 
-  float m_run = -INFINITY; // per head n (lanes with the same n agree)
+  float m_run = -INFINITY; // for head n (head lanes)
   float l_run = 0.f;       // per-lane partial sum for head n
   float acc[4][VEC];
 #pragma unroll
@@ -116,59 +131,58 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
   for (std::size_t c0 = begin + static_cast<std::size_t>(wave) * 32; c0 < end;
        c0 += static_cast<std::size_t>(WAVES) * 32) {
     // Issue every load of the chunk first: K for the scores, V for the slice.
-    u32x4 kv[2][8];
+    // Tokens past `end` read row end-1 (in bounds); they are masked below.
+    u32x4 kr[4][4];
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      // Tokens past `end` read row end-1 (in bounds); their scores are masked.
-      std::size_t tok = c0 + 16 * g + n;
+    for (int g = 0; g < 4; ++g) {
+      std::size_t tok = c0 + 8 * g + rt;
       tok = tok < end ? tok : end - 1;
       const bf16_bits *row = tok == pos ? a.key_new + kv_head * kHeadDim
                                         : kplane + cache_row(a.head_major, tok, kv_head, a.max_ctx);
 #pragma unroll
-      for (int kb = 0; kb < 8; ++kb)
-        kv[g][kb] = *reinterpret_cast<const u32x4 *>(row + kb * 32 + kq * 8);
+      for (int line = 0; line < 4; ++line)
+        kr[g][line] = *reinterpret_cast<const u32x4 *>(row + line * 64 + seg * 8);
     }
     VRow<VEC> vv[TPL];
 #pragma unroll
     for (int j = 0; j < TPL; ++j) {
-      // Tokens past `end` read row end-1; their probability is zero.
       std::size_t tok = c0 + tl + TL * j;
       tok = tok < end ? tok : end - 1;
       const bf16_bits *row = tok == pos ? a.value_new + kv_head * kHeadDim
                                         : vplane + cache_row(a.head_major, tok, kv_head, a.max_ctx);
       vv[j].load(row + dq * DIMS + VEC * dl);
     }
-    // Scores: tile g holds S[token 16g + kq*4 + i][head n].
-    floatx4 s[2];
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      s[g] = floatx4{};
-#pragma unroll
-      for (int kb = 0; kb < 8; ++kb)
-        s[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kv[g][kb]), qb[kb],
-                                                       s[g], 0, 0, 0);
-    }
+    // Scores of tokens c0 + 8g + 2kq + {0, 1} for head n (head lanes).
+    float sg[4][2];
     float mx = -INFINITY;
 #pragma unroll
-    for (int g = 0; g < 2; ++g)
+    for (int g = 0; g < 4; ++g) {
+      floatx4 c = floatx4{};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const std::size_t tok = c0 + 16 * g + kq * 4 + i;
-        s[g][i] = tok < end ? s[g][i] * scale : -INFINITY;
-        mx = fmaxf(mx, s[g][i]);
-      }
+      for (int line = 0; line < 4; ++line)
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[g][line]), qb[line], c,
+                                                    0, 0, 0);
+      // Scaled on VALU first, so the DPP reads a VALU result, not an MFMA one.
+      const float s0 = c[0] * scale + dpp<kDppRor12>(c[1] * scale);
+      const float s1 = c[2] * scale + dpp<kDppRor12>(c[3] * scale);
+      const std::size_t t0 = c0 + 8 * g + 2 * kq;
+      sg[g][0] = head_lane && t0 < end ? s0 : -INFINITY;
+      sg[g][1] = head_lane && t0 + 1 < end ? s1 : -INFINITY;
+      mx = fmaxf(mx, fmaxf(sg[g][0], sg[g][1]));
+    }
     mx = fmaxf(mx, xor16(mx));
     mx = fmaxf(mx, xor32(mx));
+    // Lanes that hold no head see m_new = -inf; their values are never used.
     const float m_new = fmaxf(m_run, mx);
     const float sc = fast_exp2(m_run - m_new); // m_run = -inf -> 0
     float psum = 0.f;
 #pragma unroll
-    for (int g = 0; g < 2; ++g)
+    for (int g = 0; g < 4; ++g)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p = fast_exp2(s[g][i] - m_new);
+      for (int t = 0; t < 2; ++t) {
+        const float p = fast_exp2(sg[g][t] - m_new);
         psum += p;
-        if (n < kGroup) sh.p[wave][16 * g + kq * 4 + i][n] = p;
+        if (head_lane) sh.p[wave][8 * g + 2 * kq + t][n] = p;
       }
     l_run = l_run * sc + psum;
     m_run = m_new;
@@ -195,25 +209,46 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
     }
     wave_lds_order();
   }
-  // Sum l over the four row-quarters (lanes n, n+16, n+32, n+48).
+  // l: the lanes of head n are n, n+16, n+32, n+48.
   float l_tot = l_run + xor16(l_run);
   l_tot += xor32(l_tot);
-  // Sum acc over the token phases (lanes differing in bits >= log2(DP)).
-#pragma unroll
-  for (int off = DL; off < 64; off <<= 1)
-#pragma unroll
-    for (int h = 0; h < 4; ++h)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[h][e] += __shfl_xor(acc[h][e], off);
   if (lane < kGroup) {
     sh.m[wave][lane] = m_run;
     sh.l[wave][lane] = l_tot;
   }
-  if (tl == 0) {
+  // Sum acc over the token phases (lane bits >= log2(DL)) by reduce-scatter:
+  // value v = h*VEC + e; after the lane-32 step lane bit 5 selects the upper
+  // half of the values, after the lane-16 step bit 4 the upper quarter, so
+  // lane l ends with values i + NV/4 * b4 + NV/2 * b5 (or i + NV/2 * b5).
+  constexpr int NV = 4 * VEC;
+  float v[NV];
 #pragma unroll
-    for (int h = 0; h < 4; ++h)
+  for (int h = 0; h < 4; ++h)
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) sh.acc[wave][h][VEC * dl + e] = acc[h][e];
+    for (int e = 0; e < VEC; ++e) v[h * VEC + e] = acc[h][e];
+#pragma unroll
+  for (int i = 0; i < NV / 2; ++i) v[i] = swap_sum32(v[i], v[i + NV / 2]);
+  const int b5 = (lane >> 5) & 1, b4 = (lane >> 4) & 1;
+  if constexpr (TL >= 4) {
+#pragma unroll
+    for (int i = 0; i < NV / 4; ++i) v[i] = swap_sum16(v[i], v[i + NV / 4]);
+    if constexpr (TL == 8) {
+#pragma unroll
+      for (int i = 0; i < NV / 4; ++i) v[i] = sum_xor8(v[i]);
+    }
+    if (TL < 8 || (lane & 8) == 0) {
+#pragma unroll
+      for (int i = 0; i < NV / 4; ++i) {
+        const int idx = i + (NV / 4) * b4 + (NV / 2) * b5;
+        sh.acc[wave][idx / VEC][VEC * dl + idx % VEC] = v[i];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NV / 2; ++i) {
+      const int idx = i + (NV / 2) * b5;
+      sh.acc[wave][idx / VEC][VEC * dl + idx % VEC] = v[i];
+    }
   }
 }
 
