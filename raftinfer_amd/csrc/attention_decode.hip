@@ -200,46 +200,47 @@ __global__ __launch_bounds__(WAVES * 64) void decode_partition_kernel(
 // partitions are independent.  A device position needing more partitions than
 // the plan's capacity writes NaN and counts a capacity error instead of
 // trapping.
-constexpr int kMergeChunk = 256;
+constexpr int kMergeChunk = 32;
 
+// Merges the partials of one head online over chunks of kMergeChunk
+// partitions; thread d owns output dim d.  Lane u of every wave reads the
+// max and sum of partition base + u, the chunk max and the sum of weighted
+// sums are lane reductions, and lane u's weight reaches the other lanes by
+// v_readlane.  Every load of a chunk is issued before any is used, so a
+// chunk costs one memory round trip.
 __device__ __forceinline__ void merge_head(const float *__restrict__ pmax,
                                            const float *__restrict__ psum,
                                            const float *__restrict__ pval, std::size_t first,
                                            std::size_t active, float &l_out, float &a_out) {
-  __shared__ float w_sh[kMergeChunk];
-  __shared__ float red[4];
   const int d = threadIdx.x;
-  float mm = -INFINITY;
-  for (std::size_t p = d; p < active; p += 256) mm = fmaxf(mm, pmax[first + p]);
-  mm = wave_max(mm);
-  if ((d & 63) == 0) red[d >> 6] = mm;
-  __syncthreads();
-  mm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  float l = 0.f, a = 0.f;
+  const int lane = d & 63;
+  float m = -INFINITY, l = 0.f, a = 0.f;
   for (std::size_t base = 0; base < active; base += kMergeChunk) {
     const std::size_t n = active - base < kMergeChunk ? active - base : kMergeChunk;
-    __syncthreads();
-    if (static_cast<std::size_t>(d) < n) w_sh[d] = __expf(pmax[first + base + d] - mm);
-    __syncthreads();
-    float lp = 0.f;
-    if (static_cast<std::size_t>(d) < n) lp = psum[first + base + d] * w_sh[d];
-    l += lp;
-    const float *v = pval + (first + base) * kHeadDim + d;
-    std::size_t p = 0;
-    for (; p + 8 <= n; p += 8) {
-      float x[8];
+    const std::size_t pl = first + base + (static_cast<std::size_t>(lane) < n ? lane : n - 1);
+    const float mraw = pmax[pl];
+    const float sraw = psum[pl];
+    float vx[kMergeChunk];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) x[u] = v[(p + u) * kHeadDim];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) a = fmaf(x[u], w_sh[p + u], a);
+    for (int u = 0; u < kMergeChunk; ++u) {
+      const std::size_t p = first + base + (static_cast<std::size_t>(u) < n ? u : n - 1);
+      vx[u] = pval[p * kHeadDim + d];
     }
-    for (; p < n; ++p) a = fmaf(v[p * kHeadDim], w_sh[p], a);
+    const bool mine = static_cast<std::size_t>(lane) < n;
+    const float ml = mine ? mraw : -INFINITY;
+    const float cm = fmaxf(m, max_xor32(max_xor16(row16_max(ml))));
+    const float r = __expf(m - cm); // m = -inf on the first chunk -> 0
+    const float w = mine ? __expf(ml - cm) : 0.f;
+    l = fmaf(l, r, sum_xor32(sum_xor16(row16_sum(sraw * w))));
+    a *= r;
+#pragma unroll
+    for (int u = 0; u < kMergeChunk; ++u) {
+      if (static_cast<std::size_t>(u) < n)
+        a = fmaf(vx[u], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), u)), a);
+    }
+    m = cm;
   }
-  l = wave_sum(l);
-  __syncthreads();
-  if ((d & 63) == 0) red[d >> 6] = l;
-  __syncthreads();
-  l_out = red[0] + red[1] + red[2] + red[3];
+  l_out = l;
   a_out = a;
 }
 
@@ -262,9 +263,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(
     Elem<ActT>::store(output, out_idx, __builtin_nanf(""));
     return;
   }
+  const float gv = Elem<ActT>::load(gate, out_idx);
   float l, a;
   merge_head(pmax, psum, pval, head * max_partitions, active, l, a);
-  const float gv = Elem<ActT>::load(gate, out_idx);
   Elem<ActT>::store(output, out_idx, (a / l) * sigmoid_gate(gv));
 }
 
@@ -737,10 +738,11 @@ __global__ __launch_bounds__(256) void batched_merge_kernel(
   const std::size_t ctx = lengths[seq];
   if (ctx == 0 || ctx > max_ctx || ctx <= single_max) return;
   const std::size_t active = ctx / kBatchedPartition + (ctx % kBatchedPartition ? 1 : 0);
+  const std::size_t out_idx = (seq * kQueryHeads + head) * kHeadDim + threadIdx.x;
+  const float gv = Elem<ActT>::load(gate, out_idx);
   float l, a;
   merge_head(pmax, psum, pval, (seq * kQueryHeads + head) * max_partitions, active, l, a);
-  const std::size_t out_idx = (seq * kQueryHeads + head) * kHeadDim + threadIdx.x;
-  Elem<ActT>::store(output, out_idx, (a / l) * sigmoid_gate(Elem<ActT>::load(gate, out_idx)));
+  Elem<ActT>::store(output, out_idx, (a / l) * sigmoid_gate(gv));
 }
 
 // bf16 batched path: MFMA scores, dims-sliced workgroups, fused append.

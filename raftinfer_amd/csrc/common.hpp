@@ -137,6 +137,21 @@ __device__ __forceinline__ float swap_sum16(float a, float b) {
   asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
   return a + b;
 }
+// x op x[lane ^ 16] and x op x[lane ^ 32] (op = max or +) in every lane, by a
+// swap of two copies of x.
+__device__ __forceinline__ float max_xor16(float x) {
+  float a = x, b = x;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  float a = x, b = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float sum_xor16(float x) { return swap_sum16(x, x); }
+__device__ __forceinline__ float sum_xor32(float x) { return swap_sum32(x, x); }
+
 // x + x[lane ^ 8] (row_ror:8 reads lane ^ 8 of the row).
 __device__ __forceinline__ float sum_xor8(float x) { return x + dpp<0x128>(x); }
 

@@ -34,7 +34,6 @@ struct DecodeMfmaArgs {
 template <int DS, int WAVES> struct DecodeMfmaShared {
   static constexpr int DIMS = kHeadDim / DS;
   float p[WAVES][32][4];
-  float sc[WAVES][4];
   float m[WAVES][4];
   float l[WAVES][4];
   float acc[WAVES][4][DIMS];
@@ -152,6 +151,9 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
                                         : vplane + cache_row(a.head_major, tok, kv_head, a.max_ctx);
       vv[j].load(row + dq * DIMS + VEC * dl);
     }
+    // Keep every load of the chunk ahead of the first wait: the scheduler
+    // otherwise sinks V loads below the K waits, adding a second round trip.
+    __builtin_amdgcn_sched_barrier(0);
     // Scores of tokens c0 + 8g + 2kq + {0, 1} for head n (head lanes).
     float sg[4][2];
     float mx = -INFINITY;
@@ -170,8 +172,7 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
       sg[g][1] = head_lane && t0 + 1 < end ? s1 : -INFINITY;
       mx = fmaxf(mx, fmaxf(sg[g][0], sg[g][1]));
     }
-    mx = fmaxf(mx, xor16(mx));
-    mx = fmaxf(mx, xor32(mx));
+    mx = max_xor32(max_xor16(mx));
     // Lanes that hold no head see m_new = -inf; their values are never used.
     const float m_new = fmaxf(m_run, mx);
     const float sc = fast_exp2(m_run - m_new); // m_run = -inf -> 0
@@ -186,11 +187,11 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
       }
     l_run = l_run * sc + psum;
     m_run = m_new;
-    if (lane < kGroup) sh.sc[wave][lane] = sc;
     wave_lds_order();
-    float scl[4];
+    float scl[4]; // lane h < 4 holds head h's rescale factor
 #pragma unroll
-    for (int h = 0; h < 4; ++h) scl[h] = sh.sc[wave][h];
+    for (int h = 0; h < 4; ++h)
+      scl[h] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), h));
 #pragma unroll
     for (int h = 0; h < 4; ++h)
 #pragma unroll
@@ -210,8 +211,7 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
     wave_lds_order();
   }
   // l: the lanes of head n are n, n+16, n+32, n+48.
-  float l_tot = l_run + xor16(l_run);
-  l_tot += xor32(l_tot);
+  const float l_tot = sum_xor32(sum_xor16(l_run));
   if (lane < kGroup) {
     sh.m[wave][lane] = m_run;
     sh.l[wave][lane] = l_tot;
