@@ -11,6 +11,12 @@ kernel) timed alone with HIP events on its own stream; ``cpu_baseline`` times
 the CPU oracle's decode on one host core over a bounded sample.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--no-cpu] [--quick]
+    python bench.py --counters     # eager launches for rocprofv3 --pmc passes
+
+``--counters`` launches the ctx-4096 partition kernel eagerly (no graph) 20
+times on 20 distinct caches, then copies a 64 MiB buffer 20 times with a
+plain device-to-device copy kernel of known size, so that FETCH_SIZE and
+WRITE_SIZE per dispatch can be scaled by what the counters read for the copy.
 """
 from __future__ import annotations
 
@@ -47,6 +53,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline config only")
+    ap.add_argument("--counters", action="store_true",
+                    help="eager partition-kernel and copy launches for counter passes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -91,7 +99,7 @@ def main():
     results = {}
 
     # ---------------------------------------------------------- config 2
-    def split_decode(ctx, ncache):
+    def split_decode(ctx, ncache, counters=False):
         shape = ops.Qwen35AttentionShape(1, HQ, HKV, D, ctx, ctx - 1)
         caches = torch.empty(ncache, 2 * HKV * ctx * D, device="cuda", dtype=torch.bfloat16)
         for i in range(ncache):
@@ -120,11 +128,28 @@ def main():
                 ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(caches[i % ncache].data_ptr()),
                 nbytes, ctypes.c_void_p(ws.data_ptr()), ws.numel(), shape.c(), ops.DTYPE_BF16,
                 ops.CACHE_BF16, ops.HEAD_MAJOR, cplan, None, ctypes.c_void_p(stream.cuda_stream)))
+        if counters:
+            for i in range(ncache):
+                part(i)
+            torch.cuda.synchronize()
+            return None
         us = timed(call, args.steps, args.warmup)
         kus = timed_each(part, args.steps, args.warmup)
         del caches
         torch.cuda.empty_cache()
         return us, kus
+
+    if args.counters:
+        split_decode(4096, 20, counters=True)
+        src = torch.empty(64 << 20, device="cuda", dtype=torch.uint8)
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        torch.cuda.synchronize()
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("counters run: 20 partition launches (ctx 4096) + 20 copies of 64 MiB")
+        return
 
     us4096, kus4096 = split_decode(4096, 40)
     log(f"cfg2 ctx4096: {us4096:.2f} us/call, partition kernel {kus4096:.2f} us")
@@ -269,7 +294,7 @@ def main():
                    "global_batch": 1, "seq_len": 4096, "parallelism": "none (1 GPU)",
                    "decode_us_per_call": us4096,
                    "prefill_pp512_TFLOP_per_s": results.get("cfg3_prefill_pp512", {}).get("TFLOP_per_s")},
-        "roofline": {"bound": "hbm", "kernel": "decode_partition_kernel (ctx 4096)",
+        "roofline": {"bound": "hbm", "kernel": "decode_split_mfma_kernel<4, 8> (ctx 4096)",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "kernel_us": kus4096, "algorithmic_bytes": kbytes},
