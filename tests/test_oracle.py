@@ -235,3 +235,44 @@ def test_decode_plan_closed_forms():
             b = min(b, max_ctx)
             p = orc.decode_plan((1, 16, 4, 256, max_ctx), 2, ctx)
             assert p.context_bucket_tokens == b and p.active_partition_capacity == -(-b // 256)
+
+
+@pytest.mark.parametrize("tokens,hk,hv,dk,dv", [(6, 2, 4, 5, 7), (9, 1, 2, 8, 8), (4, 16, 32, 128, 128)])
+def test_delta_core_matches_reference_layer(tokens, hk, hv, dk, dv):
+    """orc_delta_core (the recurrence the GPU core kernels are checked against)
+    against the full reference layer (cpp/reference/qwen35.cpp:384-549): with a
+    width-1 conv of weight 1 the layer is silu -> l2norm -> core -> RMSNorm x w x
+    silu(z), so the core's inputs and the layer's output follow elementwise
+    from the same raw token rows.  Uses the compiled reference when built,
+    else the restatement pinned to it above."""
+    r = rng(tokens * 31 + dk)
+    hid = hv * dv
+    cd = 2 * hk * dk + hv * dv
+    stride = cd + 2 * hv + hid
+    inp = normal(r, tokens * stride).reshape(tokens, stride)
+    a_w = -np.exp(normal(r, hv))
+    dt = normal(r, hv)
+    nw = normal(r, dv)
+    rs = normal(r, hv * dk * dv, scale=0.1)
+    kw = dict(tokens=tokens, hidden=hid, hk=hk, hv=hv, dk=dk, dv=dv, width=1, eps=1e-6)
+    want, _, want_state = orc.gated_delta_prefill(
+        inp.ravel(), np.ones(cd, np.float32), a_w, dt, nw, np.zeros(0, np.float32), rs,
+        use_reference=orc.ref_lib() is not None, **kw)
+
+    x = inp.astype(np.float64)
+    silu = lambda t: t / (1 + np.exp(-t))
+    conv = silu(x[:, :cd])
+    def l2(t):
+        t = t.reshape(tokens, hk, dk)
+        return t / np.sqrt((t * t).sum(-1, keepdims=True) + 1e-6)
+    q = l2(conv[:, :hk * dk])
+    k = l2(conv[:, hk * dk:2 * hk * dk])
+    v = conv[:, 2 * hk * dk:].reshape(tokens, hv, dv)
+    beta = 1 / (1 + np.exp(-x[:, cd:cd + hv]))
+    log_decay = a_w * np.logaddexp(0, x[:, cd + hv:cd + 2 * hv] + dt)
+    raw, state = orc.delta_core(q, k, v, beta, log_decay, 1 / np.sqrt(dk), rs.reshape(hv, dk, dv))
+    raw = raw.astype(np.float64)
+    norm = raw / np.sqrt((raw * raw).mean(-1, keepdims=True) + 1e-6) * nw
+    got = norm.reshape(tokens, hid) * silu(x[:, cd + 2 * hv:])
+    np.testing.assert_allclose(got.ravel(), want, rtol=2e-4, atol=2e-5)
+    np.testing.assert_allclose(state.ravel(), want_state, rtol=2e-4, atol=2e-6)
