@@ -56,9 +56,14 @@ __host__ __device__ __forceinline__ float bf16_to_f32(bf16_bits b) {
 // Low / high bf16 of a packed dword as float.
 __device__ __forceinline__ float bf16_lo(std::uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(std::uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+// Two floats -> a packed bf16 pair by the hardware conversion
+// (v_cvt_pk_bf16_f32, round to nearest even).  Finite values and infinities
+// get exactly the bits of f32_to_bf16; a NaN stays a NaN but its payload bits
+// may differ, so cache appends (compared bit for bit) keep f32_to_bf16.
 __device__ __forceinline__ std::uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<std::uint32_t>(f32_to_bf16(lo)) |
-         (static_cast<std::uint32_t>(f32_to_bf16(hi)) << 16);
+  typedef __bf16 bf16_pair __attribute__((ext_vector_type(2)));
+  const bf16_pair v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(std::uint32_t, v);
 }
 
 // Element loads / stores from f32 or bf16 storage.
