@@ -271,7 +271,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(
 
 // ---- bf16 activations + bf16 cache: MFMA scores, dims-sliced workgroups.
 constexpr int kSplitDs = 4, kSplitWaves = 8;
-constexpr int kSingleDs = 8, kSingleMfmaWaves = 8;
+constexpr int kSingleDs = 16, kSingleMfmaWaves = 8;
 
 // Copies the new token's K and V rows of kv_head into the cache (bf16 to
 // bf16, so the stored bits equal the RNE cast of the reference's append).

@@ -638,179 +638,281 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
   if (tid < L) scratch.g[h * tokens + t0 + tid] = sh.g[tid];
 }
 
-// LDS of the chunk scan.  Every MFMA operand is read as a float4 along its
-// contraction index: lane group lk = lane/16 supplies indices 4*lk .. 4*lk+3 of
-// each 16-wide slice to four consecutive MFMAs (mfma4x4), which together sum
-// over the whole slice.
-struct ScanShared {
-  float w[kChunk][kLd];      // W rows
-  float q[kChunk][kLd];      // Q rows x q scale
-  float k[kChunk][kLd];      // K rows x k scale
-  float st[kColBlock][kLd];  // S^T: [state column][key dim]
-  float dt[kColBlock][kLdC]; // D^T: [state column][token]
-  float m[kChunk][kLdC];     // M rows
-  float g[kChunk];
-  float f[kChunk];           // e^{G_last - G_j}; 0 past the chunk end
-  float eg[kChunk];          // e^{G_i}
+// Chunk scan on bf16 MFMA with fp32-accurate products.  Every fp32 operand x
+// is split as x = xh + xl (xh = bf16(x), xl = bf16(x - xh)), and a product of
+// two split operands is taken as ah*bh + ah*bl + al*bh (the dropped al*bl is
+// below 2^-16 of it); bf16 inputs (q, k as given) have no low part.  Each term
+// is one v_mfma_f32_16x16x32_bf16 with fp32 accumulation.  The fp32 state of
+// the block's 16 columns stays in VGPRs across chunks; LDS holds its split
+// transpose as the B operand.
+//
+// MFMA 16x16x32 bf16: lane l supplies A[l%16][8*(l/16) .. +7] and
+// B[8*(l/16) .. +7][l%16], and holds C[4*(l/16) + r][l%16], r = 0..3, so A is
+// read from a row-major [m][k] tile and B from a transposed [n][k] tile, one
+// 16-byte LDS read each.
+constexpr int kLdK = kChunkDim + 8; // bf16 row stride for 128-long k
+constexpr int kLdJ = kChunk + 8;    // bf16 row stride for 64-long k
+
+struct Scan3Shared {
+  bf16_bits w[2][kChunk][kLdK];      // W (hi, lo), [i][d]
+  bf16_bits q[2][kChunk][kLdK];      // Q (hi, lo), [i][d]
+  bf16_bits kt[2][kChunkDim][kLdJ];  // K^T (hi, lo), [d][j]
+  bf16_bits m[2][kChunk][kLdJ];      // M (hi, lo), [i][j]
+  bf16_bits st[2][kColBlock][kLdK];  // S^T (hi, lo), [c][d]
+  bf16_bits dt[2][kColBlock][kLdJ];  // D^T (hi, lo), [c][i]
+  bf16_bits ft[2][kColBlock][kLdJ];  // (e^{G_last-G} D)^T (hi, lo), [c][j]
+  float g[kChunk]; // cumulative log decay G of the chunk
 };
 
-__device__ __forceinline__ float4 lds4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
-
-__device__ __forceinline__ floatx4 mfma4x4(float4 a, float4 b, floatx4 c) {
-  c = mfma4(a.x, b.x, c);
-  c = mfma4(a.y, b.y, c);
-  c = mfma4(a.z, b.z, c);
-  return mfma4(a.w, b.w, c);
+__device__ __forceinline__ bf16x8 lds8(const bf16_bits *p) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(p));
+}
+__device__ __forceinline__ floatx4 mfma_bf16(const bf16_bits *a, const bf16_bits *b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(lds8(a), lds8(b), c, 0, 0, 0);
+}
+// Split of a float pair into packed (hi, lo) bf16 pairs.
+__device__ __forceinline__ void split2(float a, float b, std::uint32_t &h, std::uint32_t &l) {
+  h = pack_bf16x2(a, b);
+  l = pack_bf16x2(a - bf16_lo(h), b - bf16_hi(h));
 }
 
-// All global inputs of one chunk, held in registers so the next chunk's loads
-// are in flight while the current chunk is computed.
-template <typename InT> struct ScanChunk {
-  RowBlock<float> w;
-  RowBlock<InT> q, k;
-  float4 m[4];
-  floatx4 u; // U[wave*16 + lk*4 + r][c0 + lr]
+// Element e (0..7) of row slot r of a RowBlock.
+__device__ __forceinline__ float row_get(const RowBlock<float> &b, int r, int e) {
+  const float4 v = b.c[r][e >> 2];
+  switch (e & 3) {
+  case 0: return v.x; case 1: return v.y; case 2: return v.z; default: return v.w;
+  }
+}
+__device__ __forceinline__ float row_get(const RowBlock<bf16_bits> &b, int r, int e) {
+  return b.c[r].get(e);
+}
+// Splits elements 0..7 of row slot r into packed (hi, lo) bf16 pairs.
+template <typename T>
+__device__ __forceinline__ void split_row(const RowBlock<T> &b, int r, u32x4 &hi, u32x4 &lo) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    std::uint32_t h, l;
+    split2(row_get(b, r, 2 * e), row_get(b, r, 2 * e + 1), h, l);
+    hi[e] = h;
+    lo[e] = l;
+  }
+}
+
+// One chunk's global inputs, held in registers so the next chunk's loads are
+// in flight while the current chunk is computed.
+template <typename InT> struct ScanRegs {
+  RowBlock<float> w;  // rows (tid + 256 r) / 16, dims 8 ((tid + 256 r) % 16)
+  RowBlock<InT> q;
+  Chunk8<InT> k[2][2]; // K rows 2 jp, 2 jp + 1 of item r: jp = item % 32, dims 8 (item / 32)
+  float4 m[4];         // M rows (tid + 256 r) / 16, columns 4 ((tid + 256 r) % 16)
+  floatx4 u;           // U[16 wave + 4 (lane / 16) + r][c0 + lane % 16]
   float g;
   __device__ __forceinline__ void load(const Src<InT> &qs, const Src<InT> &ks,
                                        const ChunkScratch &sc, std::size_t h, std::size_t kh,
                                        std::size_t tokens, std::size_t t0, int c0) {
     const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    w.load(L, [&](int i, int d) { return sc.w + (h * tokens + t0 + i) * kChunkDim + d; });
+    const float *wbase = sc.w + (h * tokens + t0) * kChunkDim;
+    w.load(L, [&](int i, int d) { return wbase + i * kChunkDim + d; });
     q.load(L, [&](int i, int d) { return src_row(qs, t0 + i, kh, d); });
-    k.load(L, [&](int i, int d) { return src_row(ks, t0 + i, kh, d); });
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int item = tid + 256 * r;
+      const int j0 = 2 * (item & 31), d = 8 * (item >> 5);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        // Rows past L load row L-1 (in bounds); their decay factor f is 0.
+        const int j = j0 + e < L ? j0 + e : L - 1;
+        k[r][e].load(src_row(ks, t0 + j, kh, d));
+      }
+    }
+    const float *mbase = sc.m + (h * tokens + t0) * kChunk;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int p = tid + 256 * r;
       const int i = p >> 4, j = 4 * (p & 15);
-      m[r] = *reinterpret_cast<const float4 *>(sc.m + (h * tokens + t0 + (i < L ? i : L - 1)) * kChunk + j);
+      m[r] = *reinterpret_cast<const float4 *>(mbase + (i < L ? i : L - 1) * kChunk + j);
     }
+    const float *ubase = sc.u + (h * tokens + t0) * kChunkDim + c0 + (lane & 15);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = wave * 16 + (lane >> 4) * 4 + r;
-      u[r] = sc.u[(h * tokens + t0 + (i < L ? i : L - 1)) * kChunkDim + c0 + (lane & 15)];
+      u[r] = ubase[(i < L ? i : L - 1) * kChunkDim];
     }
     g = sc.g[h * tokens + t0 + (tid < L ? tid : L - 1)];
   }
-  __device__ __forceinline__ void store(ScanShared &sh, float qscale, float kscale) const {
+
+  __device__ __forceinline__ void store(Scan3Shared &sh) const {
     const int tid = threadIdx.x;
-    w.store(sh.w, 1.0f);
-    q.store(sh.q, qscale);
-    k.store(sh.k, kscale);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int p = tid + 256 * r;
-      *reinterpret_cast<float4 *>(&sh.m[p >> 4][4 * (p & 15)]) = m[r];
+      const int i = p >> 4, d = 8 * (p & 15);
+      u32x4 hi, lo;
+      split_row(w, r, hi, lo);
+      *reinterpret_cast<u32x4 *>(&sh.w[0][i][d]) = hi;
+      *reinterpret_cast<u32x4 *>(&sh.w[1][i][d]) = lo;
+      if constexpr (std::is_same_v<InT, bf16_bits>) {
+        *reinterpret_cast<u32x4 *>(&sh.q[0][i][d]) = q.c[r].w;
+      } else {
+        split_row(q, r, hi, lo);
+        *reinterpret_cast<u32x4 *>(&sh.q[0][i][d]) = hi;
+        *reinterpret_cast<u32x4 *>(&sh.q[1][i][d]) = lo;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int item = tid + 256 * r;
+      const int j0 = 2 * (item & 31), d = 8 * (item >> 5);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if constexpr (std::is_same_v<InT, bf16_bits>) {
+          const std::uint32_t a = (k[r][0].w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+          const std::uint32_t b = (k[r][1].w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+          *reinterpret_cast<std::uint32_t *>(&sh.kt[0][d + e][j0]) = a | (b << 16);
+        } else {
+          std::uint32_t hi, lo;
+          split2(k[r][0].get(e), k[r][1].get(e), hi, lo);
+          *reinterpret_cast<std::uint32_t *>(&sh.kt[0][d + e][j0]) = hi;
+          *reinterpret_cast<std::uint32_t *>(&sh.kt[1][d + e][j0]) = lo;
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int p = tid + 256 * r;
+      const int i = p >> 4, j = 4 * (p & 15);
+      std::uint32_t h0, l0, h1, l1;
+      split2(m[r].x, m[r].y, h0, l0);
+      split2(m[r].z, m[r].w, h1, l1);
+      *reinterpret_cast<u32x2 *>(&sh.m[0][i][j]) = u32x2{h0, h1};
+      *reinterpret_cast<u32x2 *>(&sh.m[1][i][j]) = u32x2{l0, l1};
     }
     if (tid < kChunk) sh.g[tid] = g;
   }
 };
 
+// Writes a C-layout 16x16 fp32 tile transposed and split: lane holds rows
+// 4*(lane/16) + r of column lane%16, stored at dst[col][row0 + 4*(lane/16) ..].
+template <int LD>
+__device__ __forceinline__ void store_split_t(bf16_bits (*hi)[LD], bf16_bits (*lo)[LD], int row0,
+                                              floatx4 v) {
+  const int lane = threadIdx.x & 63;
+  std::uint32_t h0, l0, h1, l1;
+  split2(v[0], v[1], h0, l0);
+  split2(v[2], v[3], h1, l1);
+  const int c = lane & 15, rr = row0 + 4 * (lane >> 4);
+  *reinterpret_cast<u32x2 *>(&hi[c][rr]) = u32x2{h0, h1};
+  *reinterpret_cast<u32x2 *>(&lo[c][rr]) = u32x2{l0, l1};
+}
+
 // Block (value head, 16-column block), sequential over chunks.  Wave w owns
-// rows 16w.. of D and O and state rows 32w.. of the S update.
+// rows 16w.. of D and O and state rows 32w.. (two 16-row tiles) of S.
 template <typename InT, typename OutT>
 __global__ __launch_bounds__(256) void chunk_scan_kernel(Src<InT> qs, Src<InT> ks,
                                                          ChunkScratch scratch,
                                                          float *__restrict__ state,
                                                          OutT *__restrict__ out, std::size_t tokens,
                                                          std::size_t hk, std::size_t hv) {
-  __shared__ ScanShared sh;
+  constexpr bool kExactQK = std::is_same_v<InT, bf16_bits>; // q, k have no low part
+  __shared__ Scan3Shared sh;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 15, lk = lane >> 4;
   const std::size_t h = blockIdx.x;
   const std::size_t kh = h % hk;
   const int c0 = blockIdx.y * kColBlock;
   float *sg = state + h * kChunkDim * kChunkDim;
-  ScanChunk<InT> regs;
+  ScanRegs<InT> regs;
   regs.load(qs, ks, scratch, h, kh, tokens, 0, c0);
-  for (int e = tid; e < kChunkDim * kColBlock; e += 256) {
-    const int r = e / kColBlock, c = e % kColBlock;
-    sh.st[c][r] = sg[r * kChunkDim + c0 + c];
-  }
+  // fp32 state tiles: s[tt] holds S[32 wave + 16 tt + 4 lk + r][c0 + lr].
+  floatx4 s[2];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[tt][r] = sg[(32 * wave + 16 * tt + 4 * lk + r) * kChunkDim + c0 + lr];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) store_split_t<kLdK>(sh.st[0], sh.st[1], 32 * wave + 16 * tt, s[tt]);
+
   for (std::size_t t0 = 0; t0 < tokens; t0 += kChunk) {
     const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
-    __syncthreads();
-    regs.store(sh, qs.scale, ks.scale);
+    regs.store(sh);
     const floatx4 u = regs.u;
-    __syncthreads();
+    __syncthreads(); // chunk inputs and S^T in LDS
     if (t0 + kChunk < tokens) regs.load(qs, ks, scratch, h, kh, tokens, t0 + kChunk, c0);
-    if (tid < kChunk) {
-      const float gi = sh.g[tid];
-      sh.f[tid] = tid < L ? __expf(sh.g[L - 1] - gi) : 0.f;
-      sh.eg[tid] = __expf(gi);
-    }
-    // D = U - W S.
+    const int i0 = 16 * wave;
+    const float glast = sh.g[L - 1];
+    // D = U - W S for rows i0 .. i0+15 (S^T is the B operand), and
+    // D~ = e^{G_last - G} D for the S update (rows past L get weight 0).
     {
-      floatx4 a0 = floatx4{}, a1 = floatx4{};
+      floatx4 acc = floatx4{};
 #pragma unroll
       for (int kk = 0; kk < kChunkDim; kk += 32) {
-        a0 = mfma4x4(lds4(&sh.w[wave * 16 + lr][kk + 4 * lk]), lds4(&sh.st[lr][kk + 4 * lk]), a0);
-        a1 = mfma4x4(lds4(&sh.w[wave * 16 + lr][kk + 16 + 4 * lk]),
-                     lds4(&sh.st[lr][kk + 16 + 4 * lk]), a1);
+        const int ka = kk + 8 * lk;
+        acc = mfma_bf16(&sh.w[0][i0 + lr][ka], &sh.st[0][lr][ka], acc);
+        acc = mfma_bf16(&sh.w[0][i0 + lr][ka], &sh.st[1][lr][ka], acc);
+        acc = mfma_bf16(&sh.w[1][i0 + lr][ka], &sh.st[0][lr][ka], acc);
       }
-      float4 dv;
-      dv.x = u[0] - (a0[0] + a1[0]);
-      dv.y = u[1] - (a0[1] + a1[1]);
-      dv.z = u[2] - (a0[2] + a1[2]);
-      dv.w = u[3] - (a0[3] + a1[3]);
-      *reinterpret_cast<float4 *>(&sh.dt[lr][wave * 16 + lk * 4]) = dv;
+      floatx4 dv, fv;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = i0 + 4 * lk + r;
+        dv[r] = u[r] - acc[r];
+        fv[r] = i < L ? __expf(glast - sh.g[i]) * dv[r] : 0.f;
+      }
+      store_split_t<kLdJ>(sh.dt[0], sh.dt[1], i0, dv);
+      store_split_t<kLdJ>(sh.ft[0], sh.ft[1], i0, fv);
     }
-    __syncthreads();
-    // O = e^G (Q S) + M D.
+    __syncthreads(); // D^T and D~^T of every row tile written
+    // O = e^G (Q S) * q_scale + M D for rows i0 .. i0+15.
     {
       floatx4 qa = floatx4{}, ma = floatx4{};
 #pragma unroll
-      for (int kk = 0; kk < kChunkDim; kk += 16) {
-        qa = mfma4x4(lds4(&sh.q[wave * 16 + lr][kk + 4 * lk]), lds4(&sh.st[lr][kk + 4 * lk]), qa);
-        if (kk < kChunk)
-          ma = mfma4x4(lds4(&sh.m[wave * 16 + lr][kk + 4 * lk]), lds4(&sh.dt[lr][kk + 4 * lk]), ma);
+      for (int kk = 0; kk < kChunkDim; kk += 32) {
+        const int ka = kk + 8 * lk;
+        qa = mfma_bf16(&sh.q[0][i0 + lr][ka], &sh.st[0][lr][ka], qa);
+        qa = mfma_bf16(&sh.q[0][i0 + lr][ka], &sh.st[1][lr][ka], qa);
+        if constexpr (!kExactQK) qa = mfma_bf16(&sh.q[1][i0 + lr][ka], &sh.st[0][lr][ka], qa);
+      }
+#pragma unroll
+      for (int jj = 0; jj < kChunk; jj += 32) {
+        const int ja = jj + 8 * lk;
+        ma = mfma_bf16(&sh.m[0][i0 + lr][ja], &sh.dt[0][lr][ja], ma);
+        ma = mfma_bf16(&sh.m[0][i0 + lr][ja], &sh.dt[1][lr][ja], ma);
+        ma = mfma_bf16(&sh.m[1][i0 + lr][ja], &sh.dt[0][lr][ja], ma);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int i = wave * 16 + lk * 4 + r;
+        const int i = i0 + 4 * lk + r;
         if (i < L)
           Elem<OutT>::store(out, ((t0 + i) * hv + h) * kChunkDim + c0 + lr,
-                            fmaf(sh.eg[i], qa[r], ma[r]));
+                            fmaf(__expf(sh.g[i]) * qs.scale, qa[r], ma[r]));
       }
     }
-    // S'[d][c] = e^{G_last} S[d][c] + sum_j K[j][d] e^{G_last - G_j} D[j][c].
-    const float egl = sh.eg[L - 1];
-    floatx4 sn[2];
+    // S'[d][c] = e^{G_last} S[d][c] + k_scale * sum_j K[j][d] D~[j][c], rows
+    // 32 wave + 16 tt.  The fp32 state stays in registers.
+    const float egl = __expf(glast);
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      const int d0 = (2 * wave + tt) * 16;
+      const int d0 = 32 * wave + 16 * tt;
       floatx4 acc = floatx4{};
 #pragma unroll
-      for (int jj = 0; jj < kChunk; jj += 16) {
-        const int j = jj + 4 * lk;
-        const float4 fv = lds4(&sh.f[j]);
-        float4 a;
-        a.x = sh.k[j][d0 + lr] * fv.x;
-        a.y = sh.k[j + 1][d0 + lr] * fv.y;
-        a.z = sh.k[j + 2][d0 + lr] * fv.z;
-        a.w = sh.k[j + 3][d0 + lr] * fv.w;
-        acc = mfma4x4(a, lds4(&sh.dt[lr][j]), acc);
+      for (int jj = 0; jj < kChunk; jj += 32) {
+        const int ja = jj + 8 * lk;
+        acc = mfma_bf16(&sh.kt[0][d0 + lr][ja], &sh.ft[0][lr][ja], acc);
+        acc = mfma_bf16(&sh.kt[0][d0 + lr][ja], &sh.ft[1][lr][ja], acc);
+        if constexpr (!kExactQK) acc = mfma_bf16(&sh.kt[1][d0 + lr][ja], &sh.ft[0][lr][ja], acc);
       }
-      const float4 so = lds4(&sh.st[lr][d0 + lk * 4]);
-      acc[0] = fmaf(egl, so.x, acc[0]);
-      acc[1] = fmaf(egl, so.y, acc[1]);
-      acc[2] = fmaf(egl, so.z, acc[2]);
-      acc[3] = fmaf(egl, so.w, acc[3]);
-      sn[tt] = acc;
-    }
-    __syncthreads();
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      float4 v;
-      v.x = sn[tt][0]; v.y = sn[tt][1]; v.z = sn[tt][2]; v.w = sn[tt][3];
-      *reinterpret_cast<float4 *>(&sh.st[lr][(2 * wave + tt) * 16 + lk * 4]) = v;
+      for (int r = 0; r < 4; ++r) s[tt][r] = fmaf(egl, s[tt][r], ks.scale * acc[r]);
     }
+    __syncthreads(); // every wave is done reading S^T and this chunk's inputs
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) store_split_t<kLdK>(sh.st[0], sh.st[1], 32 * wave + 16 * tt, s[tt]);
   }
-  __syncthreads();
-  for (int e = tid; e < kChunkDim * kColBlock; e += 256) {
-    const int r = e / kColBlock, c = e % kColBlock;
-    sg[r * kChunkDim + c0 + c] = sh.st[c][r];
-  }
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sg[(32 * wave + 16 * tt + 4 * lk + r) * kChunkDim + c0 + lr] = s[tt][r];
 }
 
 // ----------------------------------------------------- stage 3 kernel
