@@ -42,14 +42,44 @@ constexpr int kChunkDim = 128;
 constexpr int kRecWaves = 8;
 constexpr std::size_t kChunkThreshold = 64;
 
+// Chunk records: one per (value head, 64-token chunk), written by the prep
+// kernel and streamed by the scan.  Rows past the chunk's last token are
+// padded (W, U, M rows are 0 there).  bf16 pairs are the (hi, lo) split of an
+// fp32 value: x = hi + lo with hi = bf16(x), lo = bf16(x - hi).
+namespace rec {
+constexpr std::size_t kW = 0;                                        // bf16 [2][64][128]  W
+constexpr std::size_t kQ = kW + 2 * kChunk * kChunkDim * 2;          // bf16 [2][64][128]  Q * q_scale
+constexpr std::size_t kKt = kQ + 2 * kChunk * kChunkDim * 2;         // bf16 [2][128][64]  (K * k_scale)^T
+constexpr std::size_t kM = kKt + 2 * kChunkDim * kChunk * 2;         // bf16 [2][64][64]   M
+constexpr std::size_t kU = kM + 2 * kChunk * kChunk * 2;             // f32  [64][128]     U
+constexpr std::size_t kG = kU + kChunk * kChunkDim * 4;              // f32  [64]          G (padded with G[L-1])
+constexpr std::size_t kBytes = kG + kChunk * 4;                      // 147,712
+} // namespace rec
+
+struct ChunkScratch {
+  unsigned char *rec; // [hv][chunks] records of rec::kBytes
+  std::size_t chunks;
+  __device__ __forceinline__ unsigned char *at(std::size_t h, std::size_t c) const {
+    return rec + (h * chunks + c) * rec::kBytes;
+  }
+};
+
+// Chunk records start on a 256-byte boundary after the per-token buffers.
+std::size_t record_offset(std::size_t per_token_bytes) {
+  return checked_add<Err>(per_token_bytes, 255, "gated-delta workspace byte size overflow") & ~std::size_t{255};
+}
+
+std::size_t chunk_record_bytes(std::size_t tokens, std::size_t hv, std::size_t dk, std::size_t dv) {
+  if (dk != kChunkDim || dv != kChunkDim) return 0;
+  return checked_mul<Err>(checked_mul<Err>(hv, ceil_div_unchecked(tokens, kChunk),
+                                           "gated-delta workspace shape overflow"),
+                          rec::kBytes, "gated-delta workspace shape overflow");
+}
+
 struct CheckedShape {
   std::size_t key_size, value_size, conv_dim, token_stride, convolution_elements,
       recurrent_elements, workspace_bytes;
 };
-
-std::size_t chunk_scratch_floats_per_token(std::size_t hv, std::size_t dk, std::size_t dv) {
-  return hv * (dk + dv + kChunk + 1);
-}
 
 // cpp/kernels/qwen35_delta.cu:67-135.  The workspace additionally holds
 // per-token beta / log-decay and the chunk scratch (still linear in tokens).
@@ -89,14 +119,15 @@ CheckedShape validate_shape(const GatedDeltaShape &s) {
                "gated-delta workspace shape overflow");
   const std::size_t per_token = checked_add<Err>(
       checked_add<Err>(conv_dim, s.hidden_size, "gated-delta workspace shape overflow"),
-      checked_add<Err>(checked_mul<Err>(2, s.value_heads, "gated-delta workspace shape overflow"),
-                       checked_mul<Err>(s.value_heads, s.key_dim + s.value_dim + kChunk + 1,
-                                        "gated-delta workspace shape overflow"),
-                       "gated-delta workspace shape overflow"),
+      checked_mul<Err>(2, s.value_heads, "gated-delta workspace shape overflow"),
       "gated-delta workspace shape overflow");
-  const std::size_t ws_bytes = checked_mul<Err>(
+  std::size_t ws_bytes = checked_mul<Err>(
       checked_mul<Err>(s.tokens, per_token, "gated-delta workspace shape overflow"), sizeof(float),
       "gated-delta workspace byte size overflow");
+  const std::size_t records = chunk_record_bytes(s.tokens, s.value_heads, s.key_dim, s.value_dim);
+  if (records != 0)
+    ws_bytes = checked_add<Err>(record_offset(ws_bytes), records,
+                                "gated-delta workspace byte size overflow");
   const auto int_max = static_cast<std::size_t>(std::numeric_limits<int>::max());
   require<Err>(s.tokens <= int_max, "gated-delta token count exceeds launch limit");
   require<Err>(conv_dim <= int_max, "gated-delta convolution grid overflow");
@@ -434,13 +465,6 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
 constexpr int kLd = kChunkDim + 4; // LDS row stride for 128-wide rows
 constexpr int kLdC = kChunk + 4;   // LDS row stride for 64-wide rows
 
-struct ChunkScratch {
-  float *w; // [hv][tokens][dk]
-  float *u; // [hv][tokens][dv]
-  float *m; // [hv][tokens][64]
-  float *g; // [hv][tokens] cumulative log decay within the chunk
-};
-
 // Batched staging of a 64 x 128 block of rows (rows >= L repeat row L-1): thread owns
 // rows (tid + 256 r) / 16, dims 8 * ((tid + 256 r) % 16), r = 0..3, so every
 // global load of the block is issued before any of them is consumed.
@@ -505,14 +529,44 @@ __device__ __forceinline__ const T *src_row(const Src<T> &s, std::size_t t, std:
 }
 
 struct PrepShared {
-  float k[kChunk][kLd];
-  float qv[kChunk][kLd];
-  float a[kChunk][kLdC];
-  float tm[kChunk][kLdC];
+  float k[kChunk][kLd];   // K * k_scale; later W
+  float qv[kChunk][kLd];  // Q * q_scale, then V; later U
+  float a[kChunk][kLdC];  // A
+  float tm[kChunk][kLdC]; // T = (I + A)^-1
+  float mm[kChunk][kLdC]; // M
   float g[kChunk];
   float beta[kChunk];
 };
 
+// Split of a float pair into packed (hi, lo) bf16 pairs.
+__device__ __forceinline__ void split2(float a, float b, std::uint32_t &h, std::uint32_t &l) {
+  h = pack_bf16x2(a, b);
+  l = pack_bf16x2(a - bf16_lo(h), b - bf16_hi(h));
+}
+
+// Writes a [rows][cols] fp32 LDS tile (row stride LD) to a record as split
+// bf16 [2][rows][cols], 8 elements (two 16-byte stores) per item.
+template <int LD>
+__device__ __forceinline__ void write_split_rows(const float (*src)[LD], int rows, int cols,
+                                                 bf16_bits *dst) {
+  const int per_row = cols / 8;
+  for (int item = threadIdx.x; item < rows * per_row; item += 256) {
+    const int r = item / per_row, c = 8 * (item % per_row);
+    u32x4 hi, lo;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      std::uint32_t h, l;
+      split2(src[r][c + 2 * e], src[r][c + 2 * e + 1], h, l);
+      hi[e] = h;
+      lo[e] = l;
+    }
+    *reinterpret_cast<u32x4 *>(dst + r * cols + c) = hi;
+    *reinterpret_cast<u32x4 *>(dst + rows * cols + r * cols + c) = lo;
+  }
+}
+
+// Per (value head, chunk), in parallel over chunks: the UT/WY quantities of
+// the chunk, written as one record (see rec::).
 template <typename InT>
 __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> ks, Src<InT> vs,
                                                          const float *__restrict__ beta,
@@ -526,6 +580,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
   const std::size_t kh = h % hk;
   const std::size_t t0 = static_cast<std::size_t>(blockIdx.y) * kChunk;
   const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
+  unsigned char *record = scratch.at(h, blockIdx.y);
 
   RowBlock<InT> kb, qb;
   kb.load(L, [&](int i, int d) { return src_row(ks, t0 + i, kh, d); });
@@ -537,6 +592,16 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
   }
   kb.store(sh.k, ks.scale);
   qb.store(sh.qv, qs.scale);
+  if constexpr (std::is_same_v<InT, bf16_bits>) {
+    // bf16 inputs are exact in bf16: the record keeps them unscaled (hi part
+    // only) and the scan applies q_scale / k_scale to its products.
+    bf16_bits *qr = reinterpret_cast<bf16_bits *>(record + rec::kQ);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int p = tid + 256 * r;
+      *reinterpret_cast<u32x4 *>(qr + (p >> 4) * kChunkDim + 8 * (p & 15)) = qb.c[r].w;
+    }
+  }
   RowBlock<InT> vb; // issued now, consumed after the Q-dependent products
   vb.load(L, [&](int i, int d) { return src_row(vs, t0 + i, h, d); });
   if (tid < kChunk) {
@@ -548,38 +613,46 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
     float acc = 0.f;
     for (int i = 0; i < kChunk; ++i) {
       acc += sh.g[i];
-      sh.g[i] = acc;
+      sh.g[i] = acc; // rows past L repeat G[L-1] (their g is 0)
     }
   }
   __syncthreads();
 
-  // M = e^{G_i-G_j} (q_i . k_j), j <= i  -> scratch.m; wave w = row tile w.
+  // M = e^{G_i-G_j} (q_i . k_j), j <= i, and A = beta_i e^{G_i-G_j} (k_i . k_j),
+  // j < i, on fp32 MFMA 16x16x4; wave w = row tile w.
   for (int tj = 0; tj < 4; ++tj) {
-    floatx4 acc = floatx4{};
+    floatx4 am = floatx4{}, aa = floatx4{};
     if (tj <= wave) {
 #pragma unroll 8
-      for (int k0 = 0; k0 < kChunkDim; k0 += 4)
-        acc = mfma4(sh.qv[wave * 16 + lr][k0 + lk], sh.k[tj * 16 + lr][k0 + lk], acc);
+      for (int k0 = 0; k0 < kChunkDim; k0 += 4) {
+        const float kj = sh.k[tj * 16 + lr][k0 + lk];
+        am = mfma4(sh.qv[wave * 16 + lr][k0 + lk], kj, am);
+        aa = mfma4(sh.k[wave * 16 + lr][k0 + lk], kj, aa);
+      }
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = wave * 16 + lk * 4 + r, j = tj * 16 + lr;
-      const float v = (j <= i && i < L) ? acc[r] * __expf(sh.g[i] - sh.g[j]) : 0.f;
-      if (i < L) scratch.m[(h * tokens + t0 + i) * kChunk + j] = v;
+      const float e = __expf(sh.g[i] - sh.g[j]);
+      sh.mm[i][j] = (j <= i && i < L) ? am[r] * e : 0.f;
+      sh.a[i][j] = (j < i && i < L) ? sh.beta[i] * e * aa[r] : 0.f;
     }
   }
-  // A = beta_i e^{G_i-G_j} (k_i . k_j), j < i  -> LDS.
-  for (int tj = 0; tj < 4; ++tj) {
-    floatx4 acc = floatx4{};
-    if (tj <= wave) {
-#pragma unroll 8
-      for (int k0 = 0; k0 < kChunkDim; k0 += 4)
-        acc = mfma4(sh.k[wave * 16 + lr][k0 + lk], sh.k[tj * 16 + lr][k0 + lk], acc);
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = wave * 16 + lk * 4 + r, j = tj * 16 + lr;
-      sh.a[i][j] = (j < i && i < L) ? sh.beta[i] * __expf(sh.g[i] - sh.g[j]) * acc[r] : 0.f;
+  // Q and K^T go to the record before Q's LDS is reused: fp32 inputs as
+  // (Q * q_scale, (K * k_scale)^T) split pairs, bf16 inputs unscaled.
+  constexpr bool kExact = std::is_same_v<InT, bf16_bits>;
+  if constexpr (!kExact)
+    write_split_rows<kLd>(sh.qv, kChunk, kChunkDim, reinterpret_cast<bf16_bits *>(record + rec::kQ));
+  {
+    bf16_bits *kt = reinterpret_cast<bf16_bits *>(record + rec::kKt);
+    const float kinv = kExact ? 1.0f / ks.scale : 1.0f;
+    for (int item = tid; item < kChunkDim * (kChunk / 2); item += 256) {
+      const int d = item / (kChunk / 2), j = 2 * (item % (kChunk / 2));
+      std::uint32_t hi, lo;
+      split2(sh.k[j][d] * kinv, sh.k[j + 1][d] * kinv, hi, lo);
+      *reinterpret_cast<std::uint32_t *>(kt + d * kChunk + j) = hi;
+      if constexpr (!kExact)
+        *reinterpret_cast<std::uint32_t *>(kt + kChunkDim * kChunk + d * kChunk + j) = lo;
     }
   }
   __syncthreads();
@@ -614,37 +687,56 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
     }
     __syncthreads();
   }
-  // W = T diag(beta e^G) K, U = T diag(beta) V: 4 x 8 output tiles.
-  for (int tile = wave; tile < 32; tile += 4) {
+  // W = T diag(beta e^G) K, U = T diag(beta) V: 4 x 8 output tiles, wave w
+  // takes tiles w, w+4, ...; staged through LDS (over K and V) for the
+  // row-contiguous record writes.
+  floatx4 aw[8], au[8];
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    const int tile = wave + 4 * n;
     const int ti = tile >> 3, tn = tile & 7;
-    floatx4 aw = floatx4{}, au = floatx4{};
+    aw[n] = floatx4{};
+    au[n] = floatx4{};
 #pragma unroll 4
     for (int j0 = 0; j0 < kChunk; j0 += 4) {
       const int j = j0 + lk;
       const float tmv = sh.tm[ti * 16 + lr][j];
       const float bj = sh.beta[j];
-      aw = mfma4(tmv * bj * __expf(sh.g[j]), sh.k[j][tn * 16 + lr], aw);
-      au = mfma4(tmv * bj, sh.qv[j][tn * 16 + lr], au);
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = ti * 16 + lk * 4 + r, d = tn * 16 + lr;
-      if (i < L) {
-        scratch.w[(h * tokens + t0 + i) * kChunkDim + d] = aw[r];
-        scratch.u[(h * tokens + t0 + i) * kChunkDim + d] = au[r];
-      }
+      aw[n] = mfma4(tmv * bj * __expf(sh.g[j]), sh.k[j][tn * 16 + lr], aw[n]);
+      au[n] = mfma4(tmv * bj, sh.qv[j][tn * 16 + lr], au[n]);
     }
   }
-  if (tid < L) scratch.g[h * tokens + t0 + tid] = sh.g[tid];
+  __syncthreads(); // K and V reads done
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    const int tile = wave + 4 * n;
+    const int ti = tile >> 3, tn = tile & 7;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sh.k[ti * 16 + lk * 4 + r][tn * 16 + lr] = aw[n][r];
+      sh.qv[ti * 16 + lk * 4 + r][tn * 16 + lr] = au[n][r];
+    }
+  }
+  __syncthreads();
+  write_split_rows<kLd>(sh.k, kChunk, kChunkDim, reinterpret_cast<bf16_bits *>(record + rec::kW));
+  write_split_rows<kLdC>(sh.mm, kChunk, kChunk, reinterpret_cast<bf16_bits *>(record + rec::kM));
+  {
+    float *u = reinterpret_cast<float *>(record + rec::kU);
+    for (int item = tid; item < kChunk * (kChunkDim / 4); item += 256) {
+      const int r = item / (kChunkDim / 4), c = 4 * (item % (kChunkDim / 4));
+      *reinterpret_cast<float4 *>(u + r * kChunkDim + c) =
+          make_float4(sh.qv[r][c], sh.qv[r][c + 1], sh.qv[r][c + 2], sh.qv[r][c + 3]);
+    }
+  }
+  if (tid < kChunk) reinterpret_cast<float *>(record + rec::kG)[tid] = sh.g[tid];
 }
 
-// Chunk scan on bf16 MFMA with fp32-accurate products.  Every fp32 operand x
-// is split as x = xh + xl (xh = bf16(x), xl = bf16(x - xh)), and a product of
-// two split operands is taken as ah*bh + ah*bl + al*bh (the dropped al*bl is
-// below 2^-16 of it); bf16 inputs (q, k as given) have no low part.  Each term
-// is one v_mfma_f32_16x16x32_bf16 with fp32 accumulation.  The fp32 state of
-// the block's 16 columns stays in VGPRs across chunks; LDS holds its split
-// transpose as the B operand.
+// Chunk scan on bf16 MFMA with fp32-accurate products.  The records hold
+// every fp32 operand x split as x = xh + xl, and a product of two split
+// operands is taken as ah*bh + ah*bl + al*bh (the dropped al*bl is below
+// 2^-16 of it), each term one v_mfma_f32_16x16x32_bf16 with fp32
+// accumulation.  The fp32 state of the block's 16 columns stays in VGPRs
+// across chunks; LDS holds its split transpose as the B operand.
 //
 // MFMA 16x16x32 bf16: lane l supplies A[l%16][8*(l/16) .. +7] and
 // B[8*(l/16) .. +7][l%16], and holds C[4*(l/16) + r][l%16], r = 0..3, so A is
@@ -661,7 +753,7 @@ struct Scan3Shared {
   bf16_bits st[2][kColBlock][kLdK];  // S^T (hi, lo), [c][d]
   bf16_bits dt[2][kColBlock][kLdJ];  // D^T (hi, lo), [c][i]
   bf16_bits ft[2][kColBlock][kLdJ];  // (e^{G_last-G} D)^T (hi, lo), [c][j]
-  float g[kChunk]; // cumulative log decay G of the chunk
+  float g[kChunk];                   // cumulative log decay G of the chunk
 };
 
 __device__ __forceinline__ bf16x8 lds8(const bf16_bits *p) {
@@ -670,123 +762,56 @@ __device__ __forceinline__ bf16x8 lds8(const bf16_bits *p) {
 __device__ __forceinline__ floatx4 mfma_bf16(const bf16_bits *a, const bf16_bits *b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(lds8(a), lds8(b), c, 0, 0, 0);
 }
-// Split of a float pair into packed (hi, lo) bf16 pairs.
-__device__ __forceinline__ void split2(float a, float b, std::uint32_t &h, std::uint32_t &l) {
-  h = pack_bf16x2(a, b);
-  l = pack_bf16x2(a - bf16_lo(h), b - bf16_hi(h));
-}
 
-// Element e (0..7) of row slot r of a RowBlock.
-__device__ __forceinline__ float row_get(const RowBlock<float> &b, int r, int e) {
-  const float4 v = b.c[r][e >> 2];
-  switch (e & 3) {
-  case 0: return v.x; case 1: return v.y; case 2: return v.z; default: return v.w;
-  }
-}
-__device__ __forceinline__ float row_get(const RowBlock<bf16_bits> &b, int r, int e) {
-  return b.c[r].get(e);
-}
-// Splits elements 0..7 of row slot r into packed (hi, lo) bf16 pairs.
-template <typename T>
-__device__ __forceinline__ void split_row(const RowBlock<T> &b, int r, u32x4 &hi, u32x4 &lo) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    std::uint32_t h, l;
-    split2(row_get(b, r, 2 * e), row_get(b, r, 2 * e + 1), h, l);
-    hi[e] = h;
-    lo[e] = l;
-  }
-}
-
-// One chunk's global inputs, held in registers so the next chunk's loads are
-// in flight while the current chunk is computed.
-template <typename InT> struct ScanRegs {
-  RowBlock<float> w;  // rows (tid + 256 r) / 16, dims 8 ((tid + 256 r) % 16)
-  RowBlock<InT> q;
-  Chunk8<InT> k[2][2]; // K rows 2 jp, 2 jp + 1 of item r: jp = item % 32, dims 8 (item / 32)
-  float4 m[4];         // M rows (tid + 256 r) / 16, columns 4 ((tid + 256 r) % 16)
-  floatx4 u;           // U[16 wave + 4 (lane / 16) + r][c0 + lane % 16]
+// One chunk record's operands, held in registers so the next chunk's loads
+// are in flight while the current chunk is computed.  Item n of a [2][R][C]
+// bf16 block is its 16-byte piece n (pieces are row-major, C/8 per row).
+template <bool kExact> struct ScanRegs {
+  // bf16 q / k inputs (kExact) have no low part in the record.
+  static constexpr int kQK = kExact ? 4 : 8;
+  u32x4 w[8], q[kQK], kt[kQK], m[4];
+  floatx4 u; // U[16 wave + 4 (lane / 16) + r][c0 + lane % 16]
   float g;
-  __device__ __forceinline__ void load(const Src<InT> &qs, const Src<InT> &ks,
-                                       const ChunkScratch &sc, std::size_t h, std::size_t kh,
-                                       std::size_t tokens, std::size_t t0, int c0) {
-    const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
+  __device__ __forceinline__ void load(const unsigned char *record, int c0) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float *wbase = sc.w + (h * tokens + t0) * kChunkDim;
-    w.load(L, [&](int i, int d) { return wbase + i * kChunkDim + d; });
-    q.load(L, [&](int i, int d) { return src_row(qs, t0 + i, kh, d); });
+    const u32x4 *pw = reinterpret_cast<const u32x4 *>(record + rec::kW);
+    const u32x4 *pq = reinterpret_cast<const u32x4 *>(record + rec::kQ);
+    const u32x4 *pk = reinterpret_cast<const u32x4 *>(record + rec::kKt);
+    const u32x4 *pm = reinterpret_cast<const u32x4 *>(record + rec::kM);
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int item = tid + 256 * r;
-      const int j0 = 2 * (item & 31), d = 8 * (item >> 5);
+    for (int n = 0; n < 8; ++n) w[n] = pw[tid + 256 * n];
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        // Rows past L load row L-1 (in bounds); their decay factor f is 0.
-        const int j = j0 + e < L ? j0 + e : L - 1;
-        k[r][e].load(src_row(ks, t0 + j, kh, d));
-      }
+    for (int n = 0; n < kQK; ++n) {
+      q[n] = pq[tid + 256 * n];
+      kt[n] = pk[tid + 256 * n];
     }
-    const float *mbase = sc.m + (h * tokens + t0) * kChunk;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int p = tid + 256 * r;
-      const int i = p >> 4, j = 4 * (p & 15);
-      m[r] = *reinterpret_cast<const float4 *>(mbase + (i < L ? i : L - 1) * kChunk + j);
-    }
-    const float *ubase = sc.u + (h * tokens + t0) * kChunkDim + c0 + (lane & 15);
+    for (int n = 0; n < 4; ++n) m[n] = pm[tid + 256 * n];
+    const float *pu = reinterpret_cast<const float *>(record + rec::kU) + c0 + (lane & 15);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = wave * 16 + (lane >> 4) * 4 + r;
-      u[r] = ubase[(i < L ? i : L - 1) * kChunkDim];
-    }
-    g = sc.g[h * tokens + t0 + (tid < L ? tid : L - 1)];
+    for (int r = 0; r < 4; ++r) u[r] = pu[(wave * 16 + (lane >> 4) * 4 + r) * kChunkDim];
+    g = reinterpret_cast<const float *>(record + rec::kG)[tid & (kChunk - 1)];
   }
-
   __device__ __forceinline__ void store(Scan3Shared &sh) const {
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int p = tid + 256 * r;
-      const int i = p >> 4, d = 8 * (p & 15);
-      u32x4 hi, lo;
-      split_row(w, r, hi, lo);
-      *reinterpret_cast<u32x4 *>(&sh.w[0][i][d]) = hi;
-      *reinterpret_cast<u32x4 *>(&sh.w[1][i][d]) = lo;
-      if constexpr (std::is_same_v<InT, bf16_bits>) {
-        *reinterpret_cast<u32x4 *>(&sh.q[0][i][d]) = q.c[r].w;
-      } else {
-        split_row(q, r, hi, lo);
-        *reinterpret_cast<u32x4 *>(&sh.q[0][i][d]) = hi;
-        *reinterpret_cast<u32x4 *>(&sh.q[1][i][d]) = lo;
-      }
+    for (int n = 0; n < 8; ++n) {
+      const int item = tid + 256 * n; // [2][64][16 pieces]
+      const int hl = item >> 10, row = (item >> 4) & 63, c = 8 * (item & 15);
+      *reinterpret_cast<u32x4 *>(&sh.w[hl][row][c]) = w[n];
+      if (n < kQK) *reinterpret_cast<u32x4 *>(&sh.q[hl][row][c]) = q[n];
     }
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int item = tid + 256 * r;
-      const int j0 = 2 * (item & 31), d = 8 * (item >> 5);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        if constexpr (std::is_same_v<InT, bf16_bits>) {
-          const std::uint32_t a = (k[r][0].w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-          const std::uint32_t b = (k[r][1].w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-          *reinterpret_cast<std::uint32_t *>(&sh.kt[0][d + e][j0]) = a | (b << 16);
-        } else {
-          std::uint32_t hi, lo;
-          split2(k[r][0].get(e), k[r][1].get(e), hi, lo);
-          *reinterpret_cast<std::uint32_t *>(&sh.kt[0][d + e][j0]) = hi;
-          *reinterpret_cast<std::uint32_t *>(&sh.kt[1][d + e][j0]) = lo;
-        }
-      }
+    for (int n = 0; n < kQK; ++n) {
+      const int item = tid + 256 * n; // [2][128][8 pieces]
+      const int hl = item >> 10, row = (item >> 3) & 127, c = 8 * (item & 7);
+      *reinterpret_cast<u32x4 *>(&sh.kt[hl][row][c]) = kt[n];
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int p = tid + 256 * r;
-      const int i = p >> 4, j = 4 * (p & 15);
-      std::uint32_t h0, l0, h1, l1;
-      split2(m[r].x, m[r].y, h0, l0);
-      split2(m[r].z, m[r].w, h1, l1);
-      *reinterpret_cast<u32x2 *>(&sh.m[0][i][j]) = u32x2{h0, h1};
-      *reinterpret_cast<u32x2 *>(&sh.m[1][i][j]) = u32x2{l0, l1};
+    for (int n = 0; n < 4; ++n) {
+      const int item = tid + 256 * n; // [2][64][8 pieces]
+      const int hl = item >> 9, row = (item >> 3) & 63, c = 8 * (item & 7);
+      *reinterpret_cast<u32x4 *>(&sh.m[hl][row][c]) = m[n];
     }
     if (tid < kChunk) sh.g[tid] = g;
   }
@@ -808,22 +833,20 @@ __device__ __forceinline__ void store_split_t(bf16_bits (*hi)[LD], bf16_bits (*l
 
 // Block (value head, 16-column block), sequential over chunks.  Wave w owns
 // rows 16w.. of D and O and state rows 32w.. (two 16-row tiles) of S.
-template <typename InT, typename OutT>
-__global__ __launch_bounds__(256) void chunk_scan_kernel(Src<InT> qs, Src<InT> ks,
-                                                         ChunkScratch scratch,
+template <bool kExact, typename OutT>
+__global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
                                                          float *__restrict__ state,
                                                          OutT *__restrict__ out, std::size_t tokens,
-                                                         std::size_t hk, std::size_t hv) {
-  constexpr bool kExactQK = std::is_same_v<InT, bf16_bits>; // q, k have no low part
+                                                         std::size_t hv, float q_scale,
+                                                         float k_scale) {
   __shared__ Scan3Shared sh;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 15, lk = lane >> 4;
   const std::size_t h = blockIdx.x;
-  const std::size_t kh = h % hk;
   const int c0 = blockIdx.y * kColBlock;
   float *sg = state + h * kChunkDim * kChunkDim;
-  ScanRegs<InT> regs;
-  regs.load(qs, ks, scratch, h, kh, tokens, 0, c0);
+  ScanRegs<kExact> regs;
+  regs.load(scratch.at(h, 0), c0);
   // fp32 state tiles: s[tt] holds S[32 wave + 16 tt + 4 lk + r][c0 + lr].
   floatx4 s[2];
 #pragma unroll
@@ -833,14 +856,14 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(Src<InT> qs, Src<InT> k
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) store_split_t<kLdK>(sh.st[0], sh.st[1], 32 * wave + 16 * tt, s[tt]);
 
-  for (std::size_t t0 = 0; t0 < tokens; t0 += kChunk) {
+  for (std::size_t c = 0, t0 = 0; t0 < tokens; ++c, t0 += kChunk) {
     const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
     regs.store(sh);
     const floatx4 u = regs.u;
-    __syncthreads(); // chunk inputs and S^T in LDS
-    if (t0 + kChunk < tokens) regs.load(qs, ks, scratch, h, kh, tokens, t0 + kChunk, c0);
+    __syncthreads(); // chunk operands and S^T in LDS
+    if (t0 + kChunk < tokens) regs.load(scratch.at(h, c + 1), c0);
     const int i0 = 16 * wave;
-    const float glast = sh.g[L - 1];
+    const float glast = sh.g[kChunk - 1]; // = G[L-1] (padded)
     // D = U - W S for rows i0 .. i0+15 (S^T is the B operand), and
     // D~ = e^{G_last - G} D for the S update (rows past L get weight 0).
     {
@@ -863,7 +886,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(Src<InT> qs, Src<InT> k
       store_split_t<kLdJ>(sh.ft[0], sh.ft[1], i0, fv);
     }
     __syncthreads(); // D^T and D~^T of every row tile written
-    // O = e^G (Q S) * q_scale + M D for rows i0 .. i0+15.
+    // O = e^G (Q S) + M D for rows i0 .. i0+15 (q_scale is 1 unless Q is raw bf16).
     {
       floatx4 qa = floatx4{}, ma = floatx4{};
 #pragma unroll
@@ -871,7 +894,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(Src<InT> qs, Src<InT> k
         const int ka = kk + 8 * lk;
         qa = mfma_bf16(&sh.q[0][i0 + lr][ka], &sh.st[0][lr][ka], qa);
         qa = mfma_bf16(&sh.q[0][i0 + lr][ka], &sh.st[1][lr][ka], qa);
-        if constexpr (!kExactQK) qa = mfma_bf16(&sh.q[1][i0 + lr][ka], &sh.st[0][lr][ka], qa);
+        if constexpr (!kExact) qa = mfma_bf16(&sh.q[1][i0 + lr][ka], &sh.st[0][lr][ka], qa);
       }
 #pragma unroll
       for (int jj = 0; jj < kChunk; jj += 32) {
@@ -885,11 +908,10 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(Src<InT> qs, Src<InT> k
         const int i = i0 + 4 * lk + r;
         if (i < L)
           Elem<OutT>::store(out, ((t0 + i) * hv + h) * kChunkDim + c0 + lr,
-                            fmaf(__expf(sh.g[i]) * qs.scale, qa[r], ma[r]));
+                            fmaf(__expf(sh.g[i]) * q_scale, qa[r], ma[r]));
       }
     }
-    // S'[d][c] = e^{G_last} S[d][c] + k_scale * sum_j K[j][d] D~[j][c], rows
-    // 32 wave + 16 tt.  The fp32 state stays in registers.
+    // S'[d][c] = e^{G_last} S[d][c] + sum_j K[j][d] D~[j][c], rows 32 wave + 16 tt.
     const float egl = __expf(glast);
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
@@ -900,12 +922,12 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(Src<InT> qs, Src<InT> k
         const int ja = jj + 8 * lk;
         acc = mfma_bf16(&sh.kt[0][d0 + lr][ja], &sh.ft[0][lr][ja], acc);
         acc = mfma_bf16(&sh.kt[0][d0 + lr][ja], &sh.ft[1][lr][ja], acc);
-        if constexpr (!kExactQK) acc = mfma_bf16(&sh.kt[1][d0 + lr][ja], &sh.ft[0][lr][ja], acc);
+        if constexpr (!kExact) acc = mfma_bf16(&sh.kt[1][d0 + lr][ja], &sh.ft[0][lr][ja], acc);
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s[tt][r] = fmaf(egl, s[tt][r], ks.scale * acc[r]);
+      for (int r = 0; r < 4; ++r) s[tt][r] = fmaf(egl, s[tt][r], k_scale * acc[r]);
     }
-    __syncthreads(); // every wave is done reading S^T and this chunk's inputs
+    __syncthreads(); // every wave is done reading S^T and this chunk's operands
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) store_split_t<kLdK>(sh.st[0], sh.st[1], 32 * wave + 16 * tt, s[tt]);
   }
@@ -954,7 +976,10 @@ void launch_recurrence(Src<InT> q, Src<InT> k, Src<InT> v, const float *beta, co
     chunk_prep_kernel<InT><<<pgrid, 256, 0, stream>>>(q, k, v, beta, g, scratch, tokens, hk, hv);
     check_launch<Err>("qwen35_gated_delta chunk preparation");
     const dim3 sgrid{static_cast<unsigned>(hv), kChunkDim / kColBlock, 1};
-    chunk_scan_kernel<InT, OutT><<<sgrid, 256, 0, stream>>>(q, k, scratch, state, out, tokens, hk, hv);
+    constexpr bool exact = std::is_same_v<InT, bf16_bits>;
+    chunk_scan_kernel<exact, OutT><<<sgrid, 256, 0, stream>>>(scratch, state, out, tokens, hv,
+                                                              exact ? q.scale : 1.0f,
+                                                              exact ? k.scale : 1.0f);
     check_launch<Err>("qwen35_gated_delta chunk scan");
     return;
   }
@@ -985,11 +1010,12 @@ void launch_typed(const void *input, const void *conv_weight, const void *recurr
   float *raw = convolved + s.tokens * c.conv_dim;
   float *beta = raw + s.tokens * s.hidden_size;
   float *gdecay = beta + s.tokens * s.value_heads;
-  ChunkScratch scratch;
-  scratch.w = gdecay + s.tokens * s.value_heads;
-  scratch.u = scratch.w + s.value_heads * s.tokens * s.key_dim;
-  scratch.m = scratch.u + s.value_heads * s.tokens * s.value_dim;
-  scratch.g = scratch.m + s.value_heads * s.tokens * kChunk;
+  ChunkScratch scratch{};
+  if (chunk_record_bytes(s.tokens, s.value_heads, s.key_dim, s.value_dim) != 0) {
+    scratch.rec = reinterpret_cast<unsigned char *>(ws) +
+                  record_offset(s.tokens * (c.conv_dim + s.hidden_size + 2 * s.value_heads) * sizeof(float));
+    scratch.chunks = ceil_div_unchecked(s.tokens, kChunk);
+  }
 
   const bool fast = s.key_dim == kChunkDim && s.value_dim == kChunkDim && s.conv_width == 4 &&
                     c.conv_dim % 2048 == 0 && s.hidden_size % 2048 == 0 &&
@@ -1148,10 +1174,7 @@ void qwen35_gated_delta(const void *input, const void *conv_weight, const void *
 std::size_t qwen35_gated_delta_core_workspace_bytes(GatedDeltaCoreShape s) {
   require<Err>(s.tokens > 0 && s.key_heads > 0 && s.value_heads > 0 && s.key_dim > 0 && s.value_dim > 0,
                "gated-delta core shape must be positive");
-  return checked_mul<Err>(
-      checked_mul<Err>(s.tokens, chunk_scratch_floats_per_token(s.value_heads, s.key_dim, s.value_dim),
-                       "gated-delta core workspace overflow"),
-      sizeof(float), "gated-delta core workspace overflow");
+  return chunk_record_bytes(s.tokens, s.value_heads, s.key_dim, s.value_dim);
 }
 
 void qwen35_gated_delta_core(const void *q, const void *k, const void *v, const float *beta,
@@ -1178,10 +1201,8 @@ void qwen35_gated_delta_core(const void *q, const void *k, const void *v, const 
   const Src<bf16_bits> vs{static_cast<const bf16_bits *>(v), s.value_heads * s.value_dim, s.value_dim, 1.0f};
   ChunkScratch scratch{};
   if (chunked) {
-    scratch.w = static_cast<float *>(workspace);
-    scratch.u = scratch.w + s.value_heads * s.tokens * s.key_dim;
-    scratch.m = scratch.u + s.value_heads * s.tokens * s.value_dim;
-    scratch.g = scratch.m + s.value_heads * s.tokens * kChunk;
+    scratch.rec = static_cast<unsigned char *>(workspace);
+    scratch.chunks = ceil_div_unchecked(s.tokens, kChunk);
   }
   launch_recurrence<bf16_bits, bf16_bits>(qs, ks, vs, beta, log_decay, state,
                                           static_cast<bf16_bits *>(output), scratch, s.tokens,
