@@ -528,15 +528,102 @@ __device__ __forceinline__ const T *src_row(const Src<T> &s, std::size_t t, std:
   return s.base + t * s.row + head * s.head_stride + d;
 }
 
+// T = (I + A)^-1 for a strictly lower-triangular 64 x 64 A (fp32, LDS), by
+// blocks: [[P, 0], [C, Q]]^-1 = [[P^-1, 0], [-Q^-1 C P^-1, Q^-1]].
+//   1. wave w inverts the unit lower-triangular diagonal block w (16 x 16) by
+//      substitution, lane = column (all four blocks at once);
+//   2. waves 0 and 1 form the two 16 x 16 off-diagonal blocks of the 32 x 32
+//      diagonal blocks;
+//   3. all four waves form the 32 x 32 lower-left block, one 16 x 16 tile each.
+// Products run on fp32 MFMA 16x16x4; `y` is 32 x 36 fp32 scratch.  Ends with a
+// barrier; T's strictly upper part is written as 0.
+__device__ __forceinline__ void invert_unit_lower_64(const float (*a)[kLdC], float (*tm)[kLdC],
+                                                     float (*y)[36]) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 15, lk = lane >> 4;
+  // 1. Diagonal blocks; zero the blocks right of the diagonal.
+  {
+    const int b = 16 * wave;
+    for (int j = 16 * (wave + 1) + lane; j < kChunk; j += 64)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tm[b + r][j] = 0.f;
+    if (lane < 16) {
+      float x[16], c[16][16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        x[r] = r == lane ? 1.f : 0.f;
+#pragma unroll
+        for (int j = 0; j < r; ++j) c[r][j] = a[b + r][b + j];
+      }
+#pragma unroll
+      for (int r = 1; r < 16; ++r)
+#pragma unroll
+        for (int j = 0; j < r; ++j) x[r] = fmaf(-c[r][j], x[j], x[r]);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tm[b + r][b + lane] = x[r];
+    }
+  }
+  __syncthreads();
+  // 2. Block (2p+1, 2p) = -T_qq A_qp T_pp for p = wave (waves 0, 1).
+  if (wave < 2) {
+    const int P = 32 * wave, Q = P + 16;
+    floatx4 acc = floatx4{};
+#pragma unroll
+    for (int k0 = 0; k0 < 16; k0 += 4)
+      acc = mfma4(a[Q + lr][P + k0 + lk], tm[P + k0 + lk][P + lr], acc);
+    float(*yw)[36] = y + 16 * wave;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) yw[4 * lk + r][lr] = acc[r];
+    wave_lds_order();
+    acc = floatx4{};
+#pragma unroll
+    for (int k0 = 0; k0 < 16; k0 += 4)
+      acc = mfma4(tm[Q + lr][Q + k0 + lk], yw[k0 + lk][lr], acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) tm[Q + 4 * lk + r][P + lr] = -acc[r];
+  }
+  __syncthreads();
+  // 3. Lower-left 32 x 32 block = -T_BR A_BL T_TL; wave w -> tile (2 + w/2, w%2).
+  const int ti = 2 + (wave >> 1), tj = wave & 1;
+  {
+    floatx4 acc = floatx4{};
+    for (int k0 = 16 * tj; k0 < 32; k0 += 4) // T_TL is lower triangular
+      acc = mfma4(a[16 * ti + lr][k0 + lk], tm[k0 + lk][16 * tj + lr], acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[16 * (ti - 2) + 4 * lk + r][16 * tj + lr] = acc[r];
+  }
+  __syncthreads();
+  {
+    floatx4 acc = floatx4{};
+    for (int k0 = 32; k0 < 16 * ti + 16; k0 += 4) // T_BR is lower triangular
+      acc = mfma4(tm[16 * ti + lr][k0 + lk], y[k0 - 32 + lk][16 * tj + lr], acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) tm[16 * ti + 4 * lk + r][16 * tj + lr] = -acc[r];
+  }
+  __syncthreads();
+}
+
 struct PrepShared {
   float k[kChunk][kLd];   // K * k_scale; later W
   float qv[kChunk][kLd];  // Q * q_scale, then V; later U
   float a[kChunk][kLdC];  // A
   float tm[kChunk][kLdC]; // T = (I + A)^-1
   float mm[kChunk][kLdC]; // M
+  float y[32][36];        // inverse scratch
   float g[kChunk];
   float beta[kChunk];
 };
+
+// Inclusive prefix sum over the 64 lanes of a wave (Hillis-Steele).
+__device__ __forceinline__ float wave_prefix_sum(float x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  return x;
+}
 
 // Split of a float pair into packed (hi, lo) bf16 pairs.
 __device__ __forceinline__ void split2(float a, float b, std::uint32_t &h, std::uint32_t &l) {
@@ -609,13 +696,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
     sh.g[tid] = gt;
   }
   __syncthreads();
-  if (tid == 0) {
-    float acc = 0.f;
-    for (int i = 0; i < kChunk; ++i) {
-      acc += sh.g[i];
-      sh.g[i] = acc; // rows past L repeat G[L-1] (their g is 0)
-    }
-  }
+  if (wave == 0) sh.g[lane] = wave_prefix_sum(sh.g[lane]); // rows past L repeat G[L-1] (g = 0)
   __syncthreads();
 
   // M = e^{G_i-G_j} (q_i . k_j), j <= i, and A = beta_i e^{G_i-G_j} (k_i . k_j),
@@ -657,36 +738,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
   }
   __syncthreads();
   vb.store(sh.qv, vs.scale); // Q no longer needed: stage V.
-  // T = (I + A)^-1 (A strictly lower) in 16-row blocks: for block ib,
-  // rhs = E - A[rows, 0:16ib] T[0:16ib, :] on MFMA (wave = 16-column tile),
-  // then rows r of the block: T_r = rhs_r - sum_{16ib<=j<r} A_rj T_j (wave 0,
-  // lane = column).
-  for (int ib = 0; ib < 4; ++ib) {
-    {
-      floatx4 acc = floatx4{};
-      const int cb = wave * 16;
-      for (int k0 = 0; k0 < 16 * ib; k0 += 4)
-        acc = mfma4(sh.a[16 * ib + lr][k0 + lk], sh.tm[k0 + lk][cb + lr], acc);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 16 * ib + lk * 4 + r, c = cb + lr;
-        sh.tm[row][c] = (row == c ? 1.f : 0.f) - acc[r];
-      }
-    }
-    __syncthreads();
-    if (wave == 0) {
-      float x[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float v = sh.tm[16 * ib + r][lane];
-#pragma unroll
-        for (int j = 0; j < r; ++j) v = fmaf(-sh.a[16 * ib + r][16 * ib + j], x[j], v);
-        x[r] = v;
-        sh.tm[16 * ib + r][lane] = v;
-      }
-    }
-    __syncthreads();
-  }
+  invert_unit_lower_64(sh.a, sh.tm, sh.y);
   // W = T diag(beta e^G) K, U = T diag(beta) V: 4 x 8 output tiles, wave w
   // takes tiles w, w+4, ...; staged through LDS (over K and V) for the
   // row-contiguous record writes.
@@ -726,6 +778,196 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
       const int r = item / (kChunkDim / 4), c = 4 * (item % (kChunkDim / 4));
       *reinterpret_cast<float4 *>(u + r * kChunkDim + c) =
           make_float4(sh.qv[r][c], sh.qv[r][c + 1], sh.qv[r][c + 2], sh.qv[r][c + 3]);
+    }
+  }
+  if (tid < kChunk) reinterpret_cast<float *>(record + rec::kG)[tid] = sh.g[tid];
+}
+
+// bf16 (exact) inputs: the same chunk quantities on bf16 MFMA.  q.k and k.k
+// are exact bf16 products with fp32 accumulation; the T-weighted sums
+// W = T diag(beta e^G) K and U = T diag(beta) V take the fp32 left factor as a
+// (hi, lo) split, two MFMAs per k-step.  The record holds Q and K^T unscaled.
+struct PrepBShared {
+  union {
+    struct {
+      bf16_bits q[kChunk][kChunkDim + 8];
+      bf16_bits k[kChunk][kChunkDim + 8];
+    } qk;
+    float w[kChunk][kLd]; // W staging
+    float y[32][36];      // inverse scratch (Q, K no longer needed then)
+  } r1;
+  bf16_bits kt[kChunkDim][kChunk + 8]; // K^T [d][j]
+  bf16_bits vt[kChunkDim][kChunk + 8]; // V^T [d][j]
+  union {
+    struct {
+      float a[kChunk][kLdC];
+      float tm[kChunk][kLdC];
+    } at;
+    float u[kChunk][kLd]; // U staging
+  } r3;
+  float mm[kChunk][kLdC];
+  bf16_bits tw[2][kChunk][kChunk + 8]; // T diag(beta e^G k_scale), split
+  bf16_bits tu[2][kChunk][kChunk + 8]; // T diag(beta v_scale), split
+  float g[kChunk];
+  float beta[kChunk];
+};
+
+__device__ __forceinline__ floatx4 mfma_b(const bf16_bits *a, const bf16_bits *b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+      __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(a)),
+      __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(b)), c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(256) void chunk_prep_bf16_kernel(Src<bf16_bits> qs, Src<bf16_bits> ks,
+                                                              Src<bf16_bits> vs,
+                                                              const float *__restrict__ beta,
+                                                              const float *__restrict__ gdecay,
+                                                              ChunkScratch scratch,
+                                                              std::size_t tokens, std::size_t hk,
+                                                              std::size_t hv) {
+  __shared__ PrepBShared sh;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 15, lk = lane >> 4;
+  const std::size_t h = blockIdx.x;
+  const std::size_t kh = h % hk;
+  const std::size_t t0 = static_cast<std::size_t>(blockIdx.y) * kChunk;
+  const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
+  unsigned char *record = scratch.at(h, blockIdx.y);
+
+  // Q rows: RowBlock map.  K and V: item (tid + 256 r) -> token pair
+  // 2 (item % 32) + {0, 1}, dims 8 (item / 32) .. +7, so the transposed tiles
+  // are written straight from registers, one dword (two tokens) per store.
+  // Rows past L repeat row L-1.
+  RowBlock<bf16_bits> qb;
+  qb.load(L, [&](int i, int d) { return src_row(qs, t0 + i, kh, d); });
+  Chunk8<bf16_bits> kp[2][2], vp[2][2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int item = tid + 256 * r;
+    const int j0 = 2 * (item & 31), d = 8 * (item >> 5);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int j = j0 + e < L ? j0 + e : L - 1;
+      kp[r][e].w = *reinterpret_cast<const u32x4 *>(src_row(ks, t0 + j, kh, d));
+      vp[r][e].w = *reinterpret_cast<const u32x4 *>(src_row(vs, t0 + j, h, d));
+    }
+  }
+  float bt = 0.f, gt = 0.f;
+  if (tid < L) {
+    bt = beta[(t0 + tid) * hv + h];
+    gt = gdecay[(t0 + tid) * hv + h];
+  }
+  bf16_bits *qrec = reinterpret_cast<bf16_bits *>(record + rec::kQ);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int p = tid + 256 * r;
+    const int i = p >> 4, d = 8 * (p & 15);
+    *reinterpret_cast<u32x4 *>(&sh.r1.qk.q[i][d]) = qb.c[r].w;
+    *reinterpret_cast<u32x4 *>(qrec + i * kChunkDim + d) = qb.c[r].w;
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int item = tid + 256 * r;
+    const int j0 = 2 * (item & 31), d = 8 * (item >> 5);
+    *reinterpret_cast<u32x4 *>(&sh.r1.qk.k[j0][d]) = kp[r][0].w;
+    *reinterpret_cast<u32x4 *>(&sh.r1.qk.k[j0 + 1][d]) = kp[r][1].w;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int sh16 = 16 * (e & 1);
+      const std::uint32_t k0 = (kp[r][0].w[e >> 1] >> sh16) & 0xFFFFu, k1 = (kp[r][1].w[e >> 1] >> sh16) & 0xFFFFu;
+      const std::uint32_t v0 = (vp[r][0].w[e >> 1] >> sh16) & 0xFFFFu, v1 = (vp[r][1].w[e >> 1] >> sh16) & 0xFFFFu;
+      *reinterpret_cast<std::uint32_t *>(&sh.kt[d + e][j0]) = k0 | (k1 << 16);
+      *reinterpret_cast<std::uint32_t *>(&sh.vt[d + e][j0]) = v0 | (v1 << 16);
+    }
+  }
+  if (tid < kChunk) {
+    sh.beta[tid] = bt;
+    sh.g[tid] = gt;
+  }
+  __syncthreads();
+  if (wave == 0) sh.g[lane] = wave_prefix_sum(sh.g[lane]); // rows past L repeat G[L-1] (g = 0)
+  __syncthreads();
+  {
+    bf16_bits *kr = reinterpret_cast<bf16_bits *>(record + rec::kKt);
+    for (int item = tid; item < kChunkDim * (kChunk / 8); item += 256) {
+      const int d = item >> 3, j = 8 * (item & 7);
+      *reinterpret_cast<u32x4 *>(kr + d * kChunk + j) = *reinterpret_cast<const u32x4 *>(&sh.kt[d][j]);
+    }
+  }
+  // M = e^{G_i-G_j} (q_i . k_j) q_scale k_scale (j <= i), A = beta_i e^{G_i-G_j}
+  // (k_i . k_j) k_scale^2 (j < i); wave w = row tile w, exact bf16 products.
+  const float qk_scale = qs.scale * ks.scale, kk_scale = ks.scale * ks.scale;
+  for (int tj = 0; tj < 4; ++tj) {
+    floatx4 am = floatx4{}, aa = floatx4{};
+    if (tj <= wave) {
+#pragma unroll
+      for (int kk = 0; kk < kChunkDim; kk += 32) {
+        const int ka = kk + 8 * lk;
+        am = mfma_b(&sh.r1.qk.q[wave * 16 + lr][ka], &sh.r1.qk.k[tj * 16 + lr][ka], am);
+        aa = mfma_b(&sh.r1.qk.k[wave * 16 + lr][ka], &sh.r1.qk.k[tj * 16 + lr][ka], aa);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = wave * 16 + lk * 4 + r, j = tj * 16 + lr;
+      const float e = __expf(sh.g[i] - sh.g[j]);
+      sh.mm[i][j] = (j <= i && i < L) ? am[r] * qk_scale * e : 0.f;
+      sh.r3.at.a[i][j] = (j < i && i < L) ? sh.beta[i] * e * aa[r] * kk_scale : 0.f;
+    }
+  }
+  __syncthreads();
+  invert_unit_lower_64(sh.r3.at.a, sh.r3.at.tm, sh.r1.y);
+  // tw = T diag(beta e^G k_scale), tu = T diag(beta v_scale), split.
+  for (int item = tid; item < kChunk * (kChunk / 2); item += 256) {
+    const int i = item >> 5, j = 2 * (item & 31);
+    const float t0v = sh.r3.at.tm[i][j], t1v = sh.r3.at.tm[i][j + 1];
+    const float b0 = sh.beta[j], b1 = sh.beta[j + 1];
+    std::uint32_t hi, lo;
+    split2(t0v * b0 * __expf(sh.g[j]) * ks.scale, t1v * b1 * __expf(sh.g[j + 1]) * ks.scale, hi, lo);
+    *reinterpret_cast<std::uint32_t *>(&sh.tw[0][i][j]) = hi;
+    *reinterpret_cast<std::uint32_t *>(&sh.tw[1][i][j]) = lo;
+    split2(t0v * b0 * vs.scale, t1v * b1 * vs.scale, hi, lo);
+    *reinterpret_cast<std::uint32_t *>(&sh.tu[0][i][j]) = hi;
+    *reinterpret_cast<std::uint32_t *>(&sh.tu[1][i][j]) = lo;
+  }
+  __syncthreads();
+  // W = tw K, U = tu V (B operands K^T, V^T): 4 x 8 tiles, wave w takes w + 4n.
+  floatx4 aw[8], au[8];
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    const int tile = wave + 4 * n;
+    const int ti = tile >> 3, tn = tile & 7;
+    aw[n] = floatx4{};
+    au[n] = floatx4{};
+#pragma unroll
+    for (int jj = 0; jj < kChunk; jj += 32) {
+      const int ja = jj + 8 * lk;
+      aw[n] = mfma_b(&sh.tw[0][ti * 16 + lr][ja], &sh.kt[tn * 16 + lr][ja], aw[n]);
+      aw[n] = mfma_b(&sh.tw[1][ti * 16 + lr][ja], &sh.kt[tn * 16 + lr][ja], aw[n]);
+      au[n] = mfma_b(&sh.tu[0][ti * 16 + lr][ja], &sh.vt[tn * 16 + lr][ja], au[n]);
+      au[n] = mfma_b(&sh.tu[1][ti * 16 + lr][ja], &sh.vt[tn * 16 + lr][ja], au[n]);
+    }
+  }
+  __syncthreads(); // q/k and a/tm no longer needed: stage W and U
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    const int tile = wave + 4 * n;
+    const int ti = tile >> 3, tn = tile & 7;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sh.r1.w[ti * 16 + lk * 4 + r][tn * 16 + lr] = aw[n][r];
+      sh.r3.u[ti * 16 + lk * 4 + r][tn * 16 + lr] = au[n][r];
+    }
+  }
+  __syncthreads();
+  write_split_rows<kLd>(sh.r1.w, kChunk, kChunkDim, reinterpret_cast<bf16_bits *>(record + rec::kW));
+  write_split_rows<kLdC>(sh.mm, kChunk, kChunk, reinterpret_cast<bf16_bits *>(record + rec::kM));
+  {
+    float *u = reinterpret_cast<float *>(record + rec::kU);
+    for (int item = tid; item < kChunk * (kChunkDim / 4); item += 256) {
+      const int r = item / (kChunkDim / 4), c = 4 * (item % (kChunkDim / 4));
+      *reinterpret_cast<float4 *>(u + r * kChunkDim + c) =
+          make_float4(sh.r3.u[r][c], sh.r3.u[r][c + 1], sh.r3.u[r][c + 2], sh.r3.u[r][c + 3]);
     }
   }
   if (tid < kChunk) reinterpret_cast<float *>(record + rec::kG)[tid] = sh.g[tid];
@@ -973,7 +1215,10 @@ void launch_recurrence(Src<InT> q, Src<InT> k, Src<InT> v, const float *beta, co
                        hipStream_t stream) {
   if (chunked) {
     const dim3 pgrid{static_cast<unsigned>(hv), static_cast<unsigned>(ceil_div_unchecked(tokens, kChunk)), 1};
-    chunk_prep_kernel<InT><<<pgrid, 256, 0, stream>>>(q, k, v, beta, g, scratch, tokens, hk, hv);
+    if constexpr (std::is_same_v<InT, bf16_bits>)
+      chunk_prep_bf16_kernel<<<pgrid, 256, 0, stream>>>(q, k, v, beta, g, scratch, tokens, hk, hv);
+    else
+      chunk_prep_kernel<InT><<<pgrid, 256, 0, stream>>>(q, k, v, beta, g, scratch, tokens, hk, hv);
     check_launch<Err>("qwen35_gated_delta chunk preparation");
     const dim3 sgrid{static_cast<unsigned>(hv), kChunkDim / kColBlock, 1};
     constexpr bool exact = std::is_same_v<InT, bf16_bits>;
