@@ -1014,25 +1014,35 @@ template <bool kExact> struct ScanRegs {
   u32x4 w[8], q[kQK], kt[kQK], m[4];
   floatx4 u; // U[16 wave + 4 (lane / 16) + r][c0 + lane % 16]
   float g;
-  __device__ __forceinline__ void load(const unsigned char *record, int c0) {
+  // The loads are issued in three parts, one ahead of each MFMA phase of the
+  // current chunk, so the load path works while the matrix cores do.
+  __device__ __forceinline__ void load_part(int part, const unsigned char *record, int c0) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const u32x4 *pw = reinterpret_cast<const u32x4 *>(record + rec::kW);
-    const u32x4 *pq = reinterpret_cast<const u32x4 *>(record + rec::kQ);
-    const u32x4 *pk = reinterpret_cast<const u32x4 *>(record + rec::kKt);
-    const u32x4 *pm = reinterpret_cast<const u32x4 *>(record + rec::kM);
+    if (part == 0) {
+      const u32x4 *pw = reinterpret_cast<const u32x4 *>(record + rec::kW);
 #pragma unroll
-    for (int n = 0; n < 8; ++n) w[n] = pw[tid + 256 * n];
+      for (int n = 0; n < 8; ++n) w[n] = pw[tid + 256 * n];
+      const float *pu = reinterpret_cast<const float *>(record + rec::kU) + c0 + (lane & 15);
 #pragma unroll
-    for (int n = 0; n < kQK; ++n) {
-      q[n] = pq[tid + 256 * n];
-      kt[n] = pk[tid + 256 * n];
+      for (int r = 0; r < 4; ++r) u[r] = pu[(wave * 16 + (lane >> 4) * 4 + r) * kChunkDim];
+      g = reinterpret_cast<const float *>(record + rec::kG)[tid & (kChunk - 1)];
+    } else if (part == 1) {
+      const u32x4 *pq = reinterpret_cast<const u32x4 *>(record + rec::kQ);
+      const u32x4 *pm = reinterpret_cast<const u32x4 *>(record + rec::kM);
+#pragma unroll
+      for (int n = 0; n < kQK; ++n) q[n] = pq[tid + 256 * n];
+#pragma unroll
+      for (int n = 0; n < 4; ++n) m[n] = pm[tid + 256 * n];
+    } else {
+      const u32x4 *pk = reinterpret_cast<const u32x4 *>(record + rec::kKt);
+#pragma unroll
+      for (int n = 0; n < kQK; ++n) kt[n] = pk[tid + 256 * n];
     }
-#pragma unroll
-    for (int n = 0; n < 4; ++n) m[n] = pm[tid + 256 * n];
-    const float *pu = reinterpret_cast<const float *>(record + rec::kU) + c0 + (lane & 15);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) u[r] = pu[(wave * 16 + (lane >> 4) * 4 + r) * kChunkDim];
-    g = reinterpret_cast<const float *>(record + rec::kG)[tid & (kChunk - 1)];
+  }
+  __device__ __forceinline__ void load(const unsigned char *record, int c0) {
+    load_part(0, record, c0);
+    load_part(1, record, c0);
+    load_part(2, record, c0);
   }
   __device__ __forceinline__ void store(Scan3Shared &sh) const {
     const int tid = threadIdx.x;
@@ -1103,7 +1113,9 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
     regs.store(sh);
     const floatx4 u = regs.u;
     __syncthreads(); // chunk operands and S^T in LDS
-    if (t0 + kChunk < tokens) regs.load(scratch.at(h, c + 1), c0);
+    const bool more = t0 + kChunk < tokens;
+    const unsigned char *next = scratch.at(h, more ? c + 1 : c);
+    if (more) regs.load_part(0, next, c0);
     const int i0 = 16 * wave;
     const float glast = sh.g[kChunk - 1]; // = G[L-1] (padded)
     // D = U - W S for rows i0 .. i0+15 (S^T is the B operand), and
@@ -1128,6 +1140,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
       store_split_t<kLdJ>(sh.ft[0], sh.ft[1], i0, fv);
     }
     __syncthreads(); // D^T and D~^T of every row tile written
+    if (more) regs.load_part(1, next, c0);
     // O = e^G (Q S) + M D for rows i0 .. i0+15 (q_scale is 1 unless Q is raw bf16).
     {
       floatx4 qa = floatx4{}, ma = floatx4{};
@@ -1153,6 +1166,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
                             fmaf(__expf(sh.g[i]) * q_scale, qa[r], ma[r]));
       }
     }
+    if (more) regs.load_part(2, next, c0);
     // S'[d][c] = e^{G_last} S[d][c] + sum_j K[j][d] D~[j][c], rows 32 wave + 16 tt.
     const float egl = __expf(glast);
 #pragma unroll
