@@ -92,6 +92,12 @@ typedef struct raftinfer_amd_batched_decode_shape {
   size_t sequences, max_context_tokens, cache_stride_bytes, single_block_max_tokens;
 } raftinfer_amd_batched_decode_shape;
 
+/* cpp/kernels/qwen35_primitives.cuh:34-41 */
+typedef struct raftinfer_amd_qk_norm_rope_shape {
+  size_t tokens, heads, head_dim, rotary_dim, position_offset;
+  float rope_base;
+} raftinfer_amd_qk_norm_rope_shape;
+
 typedef struct raftinfer_amd_delta_core_shape {
   size_t tokens, key_heads, value_heads, key_dim, value_dim;
 } raftinfer_amd_delta_core_shape;
@@ -210,6 +216,22 @@ int raftinfer_amd_gated_delta_core(const void *q, const void *k, const void *v, 
                                    void *output, void *workspace, size_t workspace_bytes,
                                    raftinfer_amd_delta_core_shape shape, int chunked,
                                    void *stream);
+
+/* ---- attention producers ---- */
+/* qwen35_primitives.cuh:63-67 (qwen35_qk_norm_rope; device_position may be null). */
+int raftinfer_amd_qk_norm_rope(const void *input, const void *weight, void *output,
+                               raftinfer_amd_qk_norm_rope_shape shape, float epsilon, int dtype,
+                               int weight_dtype, void *stream, const uint32_t *device_position);
+/* qwen35_primitives.cuh:93-96 (qwen35_split_full_query_gate). */
+int raftinfer_amd_split_full_query_gate(const void *query_gate, void *query, void *gate,
+                                        size_t tokens, size_t heads, size_t head_dim, int dtype,
+                                        void *stream);
+/* Additive: the split and the query's norm + RoPE in one pass. */
+int raftinfer_amd_split_query_gate_norm_rope(const void *query_gate, const void *weight,
+                                             void *query, void *gate,
+                                             raftinfer_amd_qk_norm_rope_shape shape, float epsilon,
+                                             int dtype, int weight_dtype, void *stream,
+                                             const uint32_t *device_position);
 
 #ifdef __cplusplus
 }

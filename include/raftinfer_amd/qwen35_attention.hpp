@@ -6,6 +6,7 @@
 #pragma once
 
 #include "qwen35_execution_policy.hpp"
+#include "qwen35_primitives.hpp"
 #include "tensor.h"
 
 #include <hip/hip_runtime_api.h>
@@ -15,12 +16,6 @@
 #include <string>
 
 namespace raftinfer::kernels {
-
-// cpp/kernels/qwen35_primitives.cuh:15-19
-class Qwen35PrimitiveError : public std::runtime_error {
-public:
-  explicit Qwen35PrimitiveError(const std::string &message) : std::runtime_error(message) {}
-};
 
 struct Qwen35AttentionShape {
   std::size_t tokens;

@@ -439,6 +439,32 @@ void orc_delta_core(const float *q, const float *k, const float *v,
   free(qs); free(decay); free(delta);
 }
 
+/* ------------------------------------------------ attention producers */
+void orc_qk_norm_rope(const float *input, const float *weight, float *output,
+                      size_t tokens, size_t heads, size_t head_dim,
+                      size_t rotary_dim, size_t position_offset,
+                      float rope_base, float epsilon) {
+  for (size_t t = 0; t < tokens; ++t)
+    for (size_t h = 0; h < heads; ++h) {
+      const size_t base = (t * heads + h) * head_dim;
+      rms_norm_rows(input + base, weight, output + base, 1, head_dim, epsilon);
+      partial_rope(output + base, rotary_dim, position_offset + t, rope_base);
+    }
+}
+
+void orc_split_full_query_gate(const float *query_gate, float *query,
+                               float *gate, size_t tokens, size_t heads,
+                               size_t head_dim) {
+  for (size_t t = 0; t < tokens; ++t)
+    for (size_t h = 0; h < heads; ++h)
+      for (size_t d = 0; d < head_dim; ++d) {
+        const size_t src = (t * heads + h) * 2 * head_dim + d;
+        const size_t dst = (t * heads + h) * head_dim + d;
+        query[dst] = query_gate[src];
+        gate[dst] = query_gate[src + head_dim];
+      }
+}
+
 /* ------------------------------------------------------------ metrics */
 void orc_compare(const float *c, const float *r, size_t n, double floor_,
                  double *out) {

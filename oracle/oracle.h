@@ -129,6 +129,21 @@ void orc_delta_core(const float *q, const float *k, const float *v,
 /* ---- metrics (cpp/reference/correctness.cpp:18-78) ----
  * out[0]=max_abs, out[1]=max_rel, out[2]=cosine, out[3]=nonfinite mismatches,
  * out[4]=relative L2 = ||a-b||2/||b||2 (not defined by the reference). */
+/* ---- attention producers (the step before the attention kernels) ---- */
+/* Per (token, head) vector of head_dim: RMSNorm with weight (qwen35.cpp:125-148,
+ * weight base 0), then NeoX partial RoPE at position position_offset + token
+ * (qwen35.cpp:169-186): the q/k processing of qwen35.cpp:297-312, computed by
+ * the kernel qwen35_qk_norm_rope (cpp/kernels/qwen35_primitives.cu:158-210). */
+void orc_qk_norm_rope(const float *input, const float *weight, float *output,
+                      size_t tokens, size_t heads, size_t head_dim,
+                      size_t rotary_dim, size_t position_offset,
+                      float rope_base, float epsilon);
+/* [tokens][heads][2][head_dim] -> query, gate [tokens][heads][head_dim]
+ * (cpp/kernels/qwen35_primitives.cu:366-386). */
+void orc_split_full_query_gate(const float *query_gate, float *query,
+                               float *gate, size_t tokens, size_t heads,
+                               size_t head_dim);
+
 void orc_compare(const float *candidate, const float *reference, size_t n,
                  double relative_floor, double *out);
 

@@ -166,6 +166,30 @@ def delta_core(q, k, v, beta, log_decay, q_scale, state):
     return raw, st
 
 
+def qk_norm_rope(x, weight, rotary_dim, position_offset, rope_base, eps, use_reference=False):
+    """x [tokens][heads][head_dim] -> RMSNorm * weight, then partial RoPE."""
+    x = f32(x)
+    tokens, heads, head_dim = x.shape
+    out = np.zeros_like(x)
+    fn = ref_lib().ref_qk_norm_rope if use_reference else lib().orc_qk_norm_rope
+    fn.argtypes = [_f] * 3 + [_sz] * 5 + [ctypes.c_float, ctypes.c_float]
+    fn.restype = ctypes.c_int if use_reference else None
+    rc = fn(_p(x), _p(f32(weight)), _p(out), tokens, heads, head_dim, rotary_dim,
+            position_offset, rope_base, eps)
+    assert rc in (None, 0)
+    return out
+
+
+def split_full_query_gate(query_gate, heads, head_dim):
+    """[tokens][heads][2][head_dim] -> (query, gate), each [tokens][heads][head_dim]."""
+    qg = f32(query_gate)
+    tokens = qg.size // (2 * heads * head_dim)
+    q = np.zeros((tokens, heads, head_dim), np.float32)
+    g = np.zeros_like(q)
+    lib().orc_split_full_query_gate(_p(qg), _p(q), _p(g), _sz(tokens), _sz(heads), _sz(head_dim))
+    return q, g
+
+
 def compare(candidate, reference, relative_floor=1e-12):
     c, r = f32(candidate).ravel(), f32(reference).ravel()
     assert c.size == r.size

@@ -63,6 +63,11 @@ class DeltaCoreShape(ctypes.Structure):
                 ("value_dim", _sz)]
 
 
+class QkNormRopeShape(ctypes.Structure):
+    _fields_ = [("tokens", _sz), ("heads", _sz), ("head_dim", _sz), ("rotary_dim", _sz),
+                ("position_offset", _sz), ("rope_base", ctypes.c_float)]
+
+
 # Every symbol include/raftinfer_amd.h declares, with its argument types.
 _I, _F = ctypes.c_int, ctypes.c_float
 _PF = ctypes.POINTER(ctypes.c_float)
@@ -104,6 +109,11 @@ SIGNATURES = {
     "raftinfer_amd_gated_delta_core_workspace_bytes": ([DeltaCoreShape, _PSZ], _I),
     "raftinfer_amd_gated_delta_core":
         ([_vp, _vp, _vp, _PF, _PF, _F, _PF, _vp, _vp, _sz, DeltaCoreShape, _I, _vp], _I),
+    "raftinfer_amd_qk_norm_rope":
+        ([_vp, _vp, _vp, QkNormRopeShape, _F, _I, _I, _vp, _vp], _I),
+    "raftinfer_amd_split_full_query_gate": ([_vp, _vp, _vp, _sz, _sz, _sz, _I, _vp], _I),
+    "raftinfer_amd_split_query_gate_norm_rope":
+        ([_vp, _vp, _vp, _vp, QkNormRopeShape, _F, _I, _I, _vp, _vp], _I),
 }
 
 _lib = None

@@ -6,6 +6,7 @@
 
 #include "raftinfer_amd/qwen35_delta.hpp"
 #include "raftinfer_amd/qwen35_online_attention.hpp"
+#include "raftinfer_amd/qwen35_primitives.hpp"
 
 #include <cstring>
 #include <exception>
@@ -273,6 +274,41 @@ int raftinfer_amd_gated_delta_core(const void *q, const void *k, const void *v, 
     qwen35_gated_delta_core(q, k, v, beta, log_decay, q_scale, state, out, ws, ws_bytes,
                             {s.tokens, s.key_heads, s.value_heads, s.key_dim, s.value_dim},
                             chunked != 0, to_stream(stream));
+  });
+}
+
+int raftinfer_amd_qk_norm_rope(const void *input, const void *weight, void *output,
+                               raftinfer_amd_qk_norm_rope_shape s, float epsilon, int dtype,
+                               int weight_dtype, void *stream, const uint32_t *device_position) {
+  return guarded([&] {
+    qwen35_qk_norm_rope(input, weight, output,
+                        {s.tokens, s.heads, s.head_dim, s.rotary_dim, s.position_offset, s.rope_base},
+                        epsilon, static_cast<RaftInferDataType>(dtype),
+                        static_cast<RaftInferDataType>(weight_dtype), to_stream(stream),
+                        device_position);
+  });
+}
+
+int raftinfer_amd_split_full_query_gate(const void *query_gate, void *query, void *gate,
+                                        size_t tokens, size_t heads, size_t head_dim, int dtype,
+                                        void *stream) {
+  return guarded([&] {
+    qwen35_split_full_query_gate(query_gate, query, gate, tokens, heads, head_dim,
+                                 static_cast<RaftInferDataType>(dtype), to_stream(stream));
+  });
+}
+
+int raftinfer_amd_split_query_gate_norm_rope(const void *query_gate, const void *weight,
+                                             void *query, void *gate,
+                                             raftinfer_amd_qk_norm_rope_shape s, float epsilon,
+                                             int dtype, int weight_dtype, void *stream,
+                                             const uint32_t *device_position) {
+  return guarded([&] {
+    qwen35_split_query_gate_norm_rope(
+        query_gate, weight, query, gate,
+        {s.tokens, s.heads, s.head_dim, s.rotary_dim, s.position_offset, s.rope_base}, epsilon,
+        static_cast<RaftInferDataType>(dtype), static_cast<RaftInferDataType>(weight_dtype),
+        to_stream(stream), device_position);
   });
 }
 

@@ -276,3 +276,42 @@ def qwen35_gated_delta_core(q, k, v, beta, log_decay, q_scale, state, output, wo
         _ptr(q), _ptr(k), _ptr(v), _fptr(beta), _fptr(log_decay), ctypes.c_float(q_scale),
         _fptr(state), _ptr(output), _ptr(workspace), _nbytes(workspace),
         DeltaCoreShape(T, hk, hv, dk, dv), int(chunked), _stream(stream)))
+
+
+# ------------------------------------------------------ attention producers
+# cpp/kernels/qwen35_primitives.cuh:34-41, :63-67, :93-96.
+@dataclass
+class QkNormRopeShape:
+    tokens: int
+    heads: int
+    head_dim: int
+    rotary_dim: int
+    position_offset: int
+    rope_base: float
+
+    def c(self):
+        return _lib.QkNormRopeShape(self.tokens, self.heads, self.head_dim, self.rotary_dim,
+                                    self.position_offset, self.rope_base)
+
+
+def qwen35_qk_norm_rope(input, weight, output, shape: QkNormRopeShape, epsilon, dtype,
+                        weight_dtype, stream=None, device_position=None) -> None:
+    _call(Qwen35PrimitiveError, _lib.load().raftinfer_amd_qk_norm_rope(
+        _ptr(input), _ptr(weight), _ptr(output), shape.c(), ctypes.c_float(epsilon), dtype,
+        weight_dtype, _stream(stream), _ptr(device_position)))
+
+
+def qwen35_split_full_query_gate(query_gate, query, gate, tokens, heads, head_dim, dtype,
+                                 stream=None) -> None:
+    _call(Qwen35PrimitiveError, _lib.load().raftinfer_amd_split_full_query_gate(
+        _ptr(query_gate), _ptr(query), _ptr(gate), tokens, heads, head_dim, dtype,
+        _stream(stream)))
+
+
+def qwen35_split_query_gate_norm_rope(query_gate, weight, query, gate, shape: QkNormRopeShape,
+                                      epsilon, dtype, weight_dtype, stream=None,
+                                      device_position=None) -> None:
+    """Additive: qwen35_split_full_query_gate then qwen35_qk_norm_rope on the query, fused."""
+    _call(Qwen35PrimitiveError, _lib.load().raftinfer_amd_split_query_gate_norm_rope(
+        _ptr(query_gate), _ptr(weight), _ptr(query), _ptr(gate), shape.c(),
+        ctypes.c_float(epsilon), dtype, weight_dtype, _stream(stream), _ptr(device_position)))

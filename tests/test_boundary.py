@@ -194,3 +194,30 @@ def test_delta_workspace_linear_and_validation():
     with pytest.raises(ops.Qwen35DeltaError, match="not dtype-aligned"):
         ops.qwen35_gated_delta(mis, f, f, f, f, f, f, f, f, one, 2, 2, stream=0x1234,
                                workspace_bytes=ws)
+
+
+def test_producer_validation_errors_before_launch():
+    # cpp/tests/qwen35_cuda_primitives_test.cu:608-660 (the qk_norm_rope cases)
+    f = FakeTensor()
+    Q = ops.QkNormRopeShape
+    inf, nan = float("inf"), float("nan")
+    cases = [(Q(1, 1, 7, 9, 0, 1e4), 1e-5, "rotary_dim exceeds head_dim"),
+             (Q(1, 1, 8, 5, 0, 1e4), 1e-5, "rotary_dim must be even"),
+             (Q(1, 1, 8, 0, 0, 1e4), 1e-5, "rotary_dim must be positive"),
+             (Q(1, 1, 8, 4, 0, inf), 1e-5, "rope_base must be finite"),
+             (Q(1, 1, 8, 4, 0, nan), 1e-5, "rope_base must be finite"),
+             (Q(1, 1, 8, 4, 0, 1e4), inf, "epsilon must be finite"),
+             (Q(1, 1, 8, 4, 0, 1e4), nan, "epsilon must be finite"),
+             (Q(2, 1, 8, 4, 2 ** 64 - 1, 1e4), 1e-5, "position range overflow"),
+             (Q(0, 1, 8, 4, 0, 1e4), 1e-5, "tokens must be positive")]
+    for shape, eps, msg in cases:
+        with pytest.raises(ops.Qwen35PrimitiveError, match=msg):
+            ops.qwen35_qk_norm_rope(f, f, f, shape, eps, 2, 2, stream=0x1234)
+    with pytest.raises(ops.Qwen35PrimitiveError, match="weight dtype is incompatible"):
+        ops.qwen35_qk_norm_rope(f, f, f, Q(1, 1, 8, 4, 0, 1e4), 1e-5, 3, 2, stream=0x1234)
+    with pytest.raises(ops.Qwen35PrimitiveError, match="unsupported Qwen3.5 primitive dtype"):
+        ops.qwen35_split_full_query_gate(f, f, f, 1, 1, 8, 7, stream=0x1234)
+    with pytest.raises(ops.Qwen35PrimitiveError, match="stream is null"):
+        ops.qwen35_split_full_query_gate(f, f, f, 1, 1, 8, 1, stream=0)
+    with pytest.raises(ops.Qwen35PrimitiveError, match="input pointer is null"):
+        ops.qwen35_split_full_query_gate(None, f, f, 1, 1, 8, 1, stream=0x1234)

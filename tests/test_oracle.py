@@ -276,3 +276,57 @@ def test_delta_core_matches_reference_layer(tokens, hk, hv, dk, dv):
     got = norm.reshape(tokens, hid) * silu(x[:, cd + 2 * hv:])
     np.testing.assert_allclose(got.ravel(), want, rtol=2e-4, atol=2e-5)
     np.testing.assert_allclose(state.ravel(), want_state, rtol=2e-4, atol=2e-6)
+
+
+# ---------------------------------------------------- attention producers
+@ref_needed
+@pytest.mark.parametrize("tokens,heads,d,rot,pos,base", [(3, 3, 13, 8, 5, 1e4), (2, 1, 256, 64, 0, 1e7),
+                                                         (4, 16, 256, 64, 1000, 1e7), (1, 2, 8, 8, 7, 10.0)])
+def test_qk_norm_rope_matches_compiled_reference(tokens, heads, d, rot, pos, base):
+    r = rng(tokens * d + rot)
+    x = normal(r, tokens * heads * d).reshape(tokens, heads, d)
+    w = normal(r, d, scale=0.5)
+    a = orc.qk_norm_rope(x, w, rot, pos, base, 1e-5)
+    b = orc.qk_norm_rope(x, w, rot, pos, base, 1e-5, use_reference=True)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_qk_norm_rope_invariants():
+    """What the mathematics fixes, independent of the restatement's code:
+    position 0 is no rotation; rotation keeps each (p, p + rot/2) pair's norm;
+    RoPE is the complex product (x_p + i x_{p+rot/2}) e^{i pos base^(-2p/rot)};
+    and after RoPE q(m).k(n) depends on m - n only."""
+    r = rng(77)
+    d, rot, base = 32, 16, 100.0
+    x = normal(r, d).reshape(1, 1, d)
+    w = normal(r, d, scale=0.5) + 1.0
+    ms = np.sqrt((x.astype(np.float64) ** 2).mean() + 1e-6)
+    normed = (x / ms * w).astype(np.float64)
+    at0 = orc.qk_norm_rope(x, w, rot, 0, base, 1e-6)
+    np.testing.assert_allclose(at0, normed, rtol=1e-6, atol=1e-6)
+    pos = 37
+    y = orc.qk_norm_rope(x, w, rot, pos, base, 1e-6)[0, 0].astype(np.float64)
+    n = normed[0, 0]
+    half = rot // 2
+    z = (n[:half] + 1j * n[half:rot]) * np.exp(1j * pos * base ** (-2.0 * np.arange(half) / rot))
+    np.testing.assert_allclose(y[:half], z.real, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(y[half:rot], z.imag, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(y[rot:], n[rot:], rtol=1e-6, atol=1e-6)  # untouched dims
+    np.testing.assert_allclose(y[:half] ** 2 + y[half:rot] ** 2, n[:half] ** 2 + n[half:rot] ** 2,
+                               rtol=1e-5)
+    q, k = normal(r, d).reshape(1, 1, d), normal(r, d).reshape(1, 1, d)
+    ones = np.ones(d, np.float32)
+    def dot(m, nn):
+        a = orc.qk_norm_rope(q, ones, rot, m, base, 1e-6)[0, 0].astype(np.float64)
+        b = orc.qk_norm_rope(k, ones, rot, nn, base, 1e-6)[0, 0].astype(np.float64)
+        return a @ b
+    assert abs(dot(10, 3) - dot(107, 100)) < 1e-4 and abs(dot(10, 3) - dot(3, 10)) > 1e-3
+
+
+def test_split_full_query_gate_layout():
+    heads, d = 3, 5
+    qg = np.arange(2 * 2 * heads * d, dtype=np.float32)  # 2 tokens
+    q, g = orc.split_full_query_gate(qg, heads, d)
+    blocks = qg.reshape(2, heads, 2, d)
+    np.testing.assert_array_equal(q, blocks[:, :, 0])
+    np.testing.assert_array_equal(g, blocks[:, :, 1])
