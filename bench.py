@@ -255,6 +255,32 @@ def main():
             "decode_step_us": us_d, "decode_GB_per_s": dbytes / us_d / 1e3}
         log(f"cfg5 delta: prefill {us_p:.1f} us, decode step {us_d:.2f} us")
 
+        # ------------------------------------- attention producers (PP512)
+        # q projection [T][16][2][256] -> split + RMSNorm + RoPE of q (fused),
+        # and RMSNorm + RoPE of k [T][4][256]; rotary 64, base 1e7.
+        T = 512
+        qg = rand_bf16(T * HQ * 2 * D)
+        kin = rand_bf16(T * HKV * D)
+        wq, wk = rand_bf16(D), rand_bf16(D)
+        qo, go = (torch.empty(T * HQ * D, device="cuda", dtype=torch.bfloat16) for _ in range(2))
+        ko = torch.empty(T * HKV * D, device="cuda", dtype=torch.bfloat16)
+        qshape = ops.QkNormRopeShape(T, HQ, D, 64, 0, 1e7)
+        kshape = ops.QkNormRopeShape(T, HKV, D, 64, 0, 1e7)
+        us_f = timed(lambda i: ops.qwen35_split_query_gate_norm_rope(
+            qg, wq, qo, go, qshape, 1e-6, 3, 3, stream=stream), args.steps, args.warmup)
+        us_k = timed(lambda i: ops.qwen35_qk_norm_rope(kin, wk, ko, kshape, 1e-6, 3, 3,
+                                                       stream=stream), args.steps, args.warmup)
+        us_s = timed(lambda i: ops.qwen35_split_full_query_gate(qg, qo, go, T, HQ, D, 3,
+                                                                stream=stream),
+                     args.steps, args.warmup)
+        fbytes = T * HQ * D * 2 * 4  # read q and gate halves, write query and gate
+        kbytes_p = T * HKV * D * 2 * 2
+        results["producers_pp512"] = {
+            "split_norm_rope_q_us": us_f, "split_norm_rope_q_GB_per_s": fbytes / us_f / 1e3,
+            "norm_rope_k_us": us_k, "norm_rope_k_GB_per_s": kbytes_p / us_k / 1e3,
+            "split_only_us": us_s, "split_only_GB_per_s": fbytes / us_s / 1e3}
+        log(f"producers PP512: fused q {us_f:.1f} us, k {us_k:.1f} us, split {us_s:.1f} us")
+
     # ------------------------------------------------------ CPU baseline
     cpu = None
     if not args.no_cpu:

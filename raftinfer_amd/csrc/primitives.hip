@@ -74,6 +74,125 @@ __global__ __launch_bounds__(kNormThreads) void norm_rope_kernel(
   }
 }
 
+// Vector of 4 consecutive elements.
+template <typename T> struct Vec4;
+template <> struct Vec4<bf16_bits> {
+  using Raw = u32x2;
+  static __device__ __forceinline__ void load(const bf16_bits *p, float (&v)[4]) {
+    const u32x2 w = *reinterpret_cast<const u32x2 *>(p);
+    v[0] = bf16_lo(w[0]); v[1] = bf16_hi(w[0]); v[2] = bf16_lo(w[1]); v[3] = bf16_hi(w[1]);
+  }
+  static __device__ __forceinline__ void store(bf16_bits *p, const float (&v)[4]) {
+    *reinterpret_cast<u32x2 *>(p) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  }
+};
+template <> struct Vec4<float> {
+  static __device__ __forceinline__ void load(const float *p, float (&v)[4]) {
+    const float4 w = *reinterpret_cast<const float4 *>(p);
+    v[0] = w.x; v[1] = w.y; v[2] = w.z; v[3] = w.w;
+  }
+  static __device__ __forceinline__ void store(float *p, const float (&v)[4]) {
+    *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+};
+template <> struct Vec4<_Float16> {
+  static __device__ __forceinline__ void load(const _Float16 *p, float (&v)[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = static_cast<float>(p[e]);
+  }
+  static __device__ __forceinline__ void store(_Float16 *p, const float (&v)[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) p[e] = static_cast<_Float16>(v[e]);
+  }
+};
+
+// head_dim 256 (the Qwen3.5 attention heads), rotary_dim a multiple of 8:
+// lane l owns dims 4l .. 4l+3 of a head vector (whole-row loads and stores);
+// the rotation partner of dims 4l.. sits in lane l +- rotary_dim/8 and comes
+// over the lane crossbar.  Rotation angles: inv_freq_p = r^p with
+// r = base^(-2/rotary_dim) (one double pow per workgroup, then double
+// products), theta = position * inv_freq_p reduced modulo 2 pi in double,
+// then a float sincos of the reduced angle.
+template <typename T, typename Wt>
+__global__ __launch_bounds__(kNormThreads) void norm_rope_256_kernel(
+    const T *__restrict__ input, const Wt *__restrict__ weight, T *__restrict__ output,
+    T *__restrict__ gate, std::size_t heads, std::size_t in_stride, std::size_t rotary_dim,
+    std::size_t position_offset, float rope_base, float epsilon,
+    const std::uint32_t *device_position) {
+  __shared__ float rot[256]; // [pairs] cos, then [pairs] sin (pairs <= 128)
+  __shared__ double ratio;
+  constexpr int kWaves = kNormThreads / 64, kBatch = 4;
+  const std::size_t token = blockIdx.x;
+  const int pairs = static_cast<int>(rotary_dim / 2);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int d0 = 4 * lane;
+  // Heads wave, wave + 4, ... in groups of four whose loads are all issued
+  // before any is used; the first group's loads go out before the angles are
+  // computed.
+  float x[kBatch][4], g[kBatch][4], w[4];
+  auto load_batch = [&](std::size_t h0) {
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const std::size_t h = h0 + kWaves * b < heads ? h0 + kWaves * b : h0;
+      const T *src = input + (token * heads + h) * in_stride;
+      Vec4<T>::load(src + d0, x[b]);
+      if (gate != nullptr) Vec4<T>::load(src + 256 + d0, g[b]);
+    }
+  };
+  if (static_cast<std::size_t>(wave) < heads) load_batch(wave);
+  Vec4<Wt>::load(weight + d0, w);
+  if (threadIdx.x == 0) ratio = pow(static_cast<double>(rope_base), -2.0 / static_cast<double>(rotary_dim));
+  __syncthreads();
+  if (static_cast<int>(threadIdx.x) < pairs) {
+    const int p = threadIdx.x;
+    double inv = 1.0, bsq = ratio;
+    for (int e = p; e != 0; e >>= 1, bsq *= bsq)
+      if (e & 1) inv *= bsq;
+    const std::size_t position =
+        (device_position != nullptr ? static_cast<std::size_t>(*device_position) : position_offset) + token;
+    const double theta = static_cast<double>(position) * inv;
+    constexpr double kTwoPi = 6.283185307179586476925286766559;
+    const double t = theta - kTwoPi * rint(theta / kTwoPi);
+    float sn, cs;
+    sincosf(static_cast<float>(t), &sn, &cs);
+    rot[p] = cs;
+    rot[pairs + p] = sn;
+  }
+  __syncthreads();
+  const int shift = pairs / 4; // lanes between a dim and its partner
+  const bool rotated = d0 < 2 * pairs, first = d0 < pairs;
+  const int src_lane = first ? lane + shift : lane - shift;
+  for (std::size_t h0 = wave; h0 < heads; h0 += kWaves * kBatch) {
+    if (h0 != static_cast<std::size_t>(wave)) load_batch(h0);
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const std::size_t h = h0 + kWaves * b;
+      if (h >= heads) break; // uniform across the wave
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss = fmaf(x[b][e], x[b][e], ss);
+      ss = wave_sum(ss);
+      const float scale = 1.0f / sqrtf(ss * (1.0f / 256.0f) + epsilon);
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = x[b][e] * scale * w[e];
+      float pv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pv[e] = __shfl(v[e], src_lane);
+      if (rotated) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int p = first ? d0 + e : d0 + e - pairs;
+          const float c = rot[p], sn = rot[pairs + p];
+          v[e] = first ? v[e] * c - pv[e] * sn : pv[e] * sn + v[e] * c;
+        }
+      }
+      Vec4<T>::store(output + (token * heads + h) * 256 + d0, v);
+      if (gate != nullptr) Vec4<T>::store(gate + (token * heads + h) * 256 + d0, g[b]);
+    }
+  }
+}
+
 // Pure copy of the two halves of each [2][head_dim] block: 16-byte pieces
 // when the rows allow it, elements otherwise.
 template <typename E>
@@ -132,6 +251,18 @@ template <typename T, typename Wt>
 void launch_norm_rope(const void *input, const void *weight, void *output, void *gate,
                       std::size_t in_stride, const QkNormRopeShape &s, float epsilon,
                       const std::uint32_t *device_position, hipStream_t stream) {
+  const std::size_t vec_bytes = 4 * sizeof(T), wvec_bytes = 4 * sizeof(Wt);
+  const auto aligned = [](const void *p, std::size_t a) {
+    return p == nullptr || (reinterpret_cast<std::uintptr_t>(p) & (a - 1)) == 0;
+  };
+  if (s.head_dim == 256 && s.rotary_dim % 8 == 0 && aligned(input, vec_bytes) &&
+      aligned(output, vec_bytes) && aligned(gate, vec_bytes) && aligned(weight, wvec_bytes)) {
+    norm_rope_256_kernel<T, Wt><<<static_cast<unsigned>(s.tokens), kNormThreads, 0, stream>>>(
+        static_cast<const T *>(input), static_cast<const Wt *>(weight), static_cast<T *>(output),
+        static_cast<T *>(gate), s.heads, in_stride, s.rotary_dim, s.position_offset, s.rope_base,
+        epsilon, device_position);
+    return;
+  }
   const std::size_t lds = (s.rotary_dim / 2) * 2 * sizeof(float);
   norm_rope_kernel<T, Wt><<<static_cast<unsigned>(s.tokens), kNormThreads, lds, stream>>>(
       static_cast<const T *>(input), static_cast<const Wt *>(weight), static_cast<T *>(output),
