@@ -226,6 +226,11 @@ int raftinfer_amd_qk_norm_rope(const void *input, const void *weight, void *outp
 int raftinfer_amd_split_full_query_gate(const void *query_gate, void *query, void *gate,
                                         size_t tokens, size_t heads, size_t head_dim, int dtype,
                                         void *stream);
+/* qwen35_primitives.cuh:98-102 (qwen35_pack_linear_delta_input). */
+int raftinfer_amd_pack_linear_delta_input(const void *qkv, const void *beta, const void *alpha,
+                                          const void *gate, void *packed, size_t tokens,
+                                          size_t qkv_width, size_t beta_width, size_t alpha_width,
+                                          size_t gate_width, int dtype, void *stream);
 /* Additive: the split and the query's norm + RoPE in one pass. */
 int raftinfer_amd_split_query_gate_norm_rope(const void *query_gate, const void *weight,
                                              void *query, void *gate,

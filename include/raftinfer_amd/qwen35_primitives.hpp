@@ -47,6 +47,14 @@ void qwen35_split_full_query_gate(const void *query_gate, void *query, void *gat
                                   std::size_t tokens, std::size_t heads, std::size_t head_dim,
                                   RaftInferDataType dtype, hipStream_t stream);
 
+// cpp/kernels/qwen35_primitives.cuh:98-102.  Each source [tokens][width];
+// packed [tokens][qkv | beta | alpha | gate], the input rows of qwen35_gated_delta.
+void qwen35_pack_linear_delta_input(const void *qkv, const void *beta, const void *alpha,
+                                    const void *gate, void *packed, std::size_t tokens,
+                                    std::size_t qkv_width, std::size_t beta_width,
+                                    std::size_t alpha_width, std::size_t gate_width,
+                                    RaftInferDataType dtype, hipStream_t stream);
+
 // Additive (no counterpart in the reference): both steps in one pass over the
 // q projection, query_gate -> RMSNorm + RoPE'd query and gate, equal to
 // qwen35_split_full_query_gate followed by qwen35_qk_norm_rope on the query.

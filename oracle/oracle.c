@@ -465,6 +465,22 @@ void orc_split_full_query_gate(const float *query_gate, float *query,
       }
 }
 
+void orc_pack_linear_delta_input(const float *qkv, const float *beta,
+                                 const float *alpha, const float *gate,
+                                 float *packed, size_t tokens, size_t qkv_width,
+                                 size_t beta_width, size_t alpha_width,
+                                 size_t gate_width) {
+  const size_t width = qkv_width + beta_width + alpha_width + gate_width;
+  for (size_t t = 0; t < tokens; ++t) {
+    float *row = packed + t * width;
+    memcpy(row, qkv + t * qkv_width, qkv_width * sizeof(float));
+    memcpy(row + qkv_width, beta + t * beta_width, beta_width * sizeof(float));
+    memcpy(row + qkv_width + beta_width, alpha + t * alpha_width, alpha_width * sizeof(float));
+    memcpy(row + qkv_width + beta_width + alpha_width, gate + t * gate_width,
+           gate_width * sizeof(float));
+  }
+}
+
 /* ------------------------------------------------------------ metrics */
 void orc_compare(const float *c, const float *r, size_t n, double floor_,
                  double *out) {

@@ -144,6 +144,14 @@ void orc_split_full_query_gate(const float *query_gate, float *query,
                                float *gate, size_t tokens, size_t heads,
                                size_t head_dim);
 
+/* Row concatenation [qkv | beta | alpha | gate] per token
+ * (cpp/kernels/qwen35_primitives.cu:388-420). */
+void orc_pack_linear_delta_input(const float *qkv, const float *beta,
+                                 const float *alpha, const float *gate,
+                                 float *packed, size_t tokens, size_t qkv_width,
+                                 size_t beta_width, size_t alpha_width,
+                                 size_t gate_width);
+
 void orc_compare(const float *candidate, const float *reference, size_t n,
                  double relative_floor, double *out);
 

@@ -190,6 +190,18 @@ def split_full_query_gate(query_gate, heads, head_dim):
     return q, g
 
 
+def pack_linear_delta_input(qkv, beta, alpha, gate):
+    """Each [tokens][width] -> [tokens][sum of widths]."""
+    parts = [f32(x) for x in (qkv, beta, alpha, gate)]
+    tokens = parts[0].shape[0]
+    widths = [x.shape[1] for x in parts]
+    out = np.zeros((tokens, sum(widths)), np.float32)
+    fn = lib().orc_pack_linear_delta_input
+    fn.restype = None
+    fn(*[_p(x) for x in parts], _p(out), _sz(tokens), *[_sz(w) for w in widths])
+    return out
+
+
 def compare(candidate, reference, relative_floor=1e-12):
     c, r = f32(candidate).ravel(), f32(reference).ravel()
     assert c.size == r.size

@@ -112,6 +112,8 @@ SIGNATURES = {
     "raftinfer_amd_qk_norm_rope":
         ([_vp, _vp, _vp, QkNormRopeShape, _F, _I, _I, _vp, _vp], _I),
     "raftinfer_amd_split_full_query_gate": ([_vp, _vp, _vp, _sz, _sz, _sz, _I, _vp], _I),
+    "raftinfer_amd_pack_linear_delta_input":
+        ([_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _I, _vp], _I),
     "raftinfer_amd_split_query_gate_norm_rope":
         ([_vp, _vp, _vp, _vp, QkNormRopeShape, _F, _I, _I, _vp, _vp], _I),
 }

@@ -298,6 +298,17 @@ int raftinfer_amd_split_full_query_gate(const void *query_gate, void *query, voi
   });
 }
 
+int raftinfer_amd_pack_linear_delta_input(const void *qkv, const void *beta, const void *alpha,
+                                          const void *gate, void *packed, size_t tokens,
+                                          size_t qkv_width, size_t beta_width, size_t alpha_width,
+                                          size_t gate_width, int dtype, void *stream) {
+  return guarded([&] {
+    qwen35_pack_linear_delta_input(qkv, beta, alpha, gate, packed, tokens, qkv_width, beta_width,
+                                   alpha_width, gate_width, static_cast<RaftInferDataType>(dtype),
+                                   to_stream(stream));
+  });
+}
+
 int raftinfer_amd_split_query_gate_norm_rope(const void *query_gate, const void *weight,
                                              void *query, void *gate,
                                              raftinfer_amd_qk_norm_rope_shape s, float epsilon,

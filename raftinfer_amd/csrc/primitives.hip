@@ -1,7 +1,7 @@
-// Attention producers for gfx950: the query/gate split of the q projection
-// and the per-head RMSNorm + NeoX partial RoPE of q and k
-// (cpp/kernels/qwen35_primitives.cu:158-210, :366-386, host :574-623,
-// :743-766).
+// Producers of the attention and delta kernels for gfx950: the query/gate
+// split of the q projection, the per-head RMSNorm + NeoX partial RoPE of q and
+// k, and the packing of the delta layer's input rows
+// (cpp/kernels/qwen35_primitives.cu:158-210, :366-420, host :574-623, :743-800).
 //
 // norm_rope_kernel: one workgroup per token.  Threads first compute the
 // rotation (cos, sin) of every pair for the token's position in double
@@ -208,6 +208,32 @@ __global__ __launch_bounds__(256) void split_kernel(const E *__restrict__ src, E
   }
 }
 
+// Row concatenation: item = (token, segment, piece); 16-byte pieces when every
+// width allows it, elements otherwise.
+template <typename E>
+__global__ __launch_bounds__(256) void pack_kernel(const E *__restrict__ s0, const E *__restrict__ s1,
+                                                   const E *__restrict__ s2, const E *__restrict__ s3,
+                                                   E *__restrict__ packed, std::size_t tokens,
+                                                   std::size_t w0, std::size_t w1, std::size_t w2,
+                                                   std::size_t w3) {
+  const std::size_t width = w0 + w1 + w2 + w3;
+  const std::size_t total = tokens * width;
+  for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * 256 + threadIdx.x; i < total;
+       i += static_cast<std::size_t>(gridDim.x) * 256) {
+    const std::size_t t = i / width, c = i - t * width;
+    E v;
+    if (c < w0)
+      v = s0[t * w0 + c];
+    else if (c < w0 + w1)
+      v = s1[t * w1 + (c - w0)];
+    else if (c < w0 + w1 + w2)
+      v = s2[t * w2 + (c - w0 - w1)];
+    else
+      v = s3[t * w3 + (c - w0 - w1 - w2)];
+    packed[i] = v;
+  }
+}
+
 void require_dtype(RaftInferDataType d) {
   require<Err>(d == RAFTINFER_DTYPE_F32 || d == RAFTINFER_DTYPE_F16 || d == RAFTINFER_DTYPE_BF16,
                "unsupported Qwen3.5 primitive dtype");
@@ -342,6 +368,57 @@ void qwen35_split_full_query_gate(const void *query_gate, void *query, void *gat
         static_cast<std::uint16_t *>(gate), vectors, head_dim);
   }
   check_launch<Err>("qwen35_split_full_query_gate");
+}
+
+void qwen35_pack_linear_delta_input(const void *qkv, const void *beta, const void *alpha,
+                                    const void *gate, void *packed, std::size_t tokens,
+                                    std::size_t qkv_width, std::size_t beta_width,
+                                    std::size_t alpha_width, std::size_t gate_width,
+                                    RaftInferDataType dtype, hipStream_t stream) {
+  // cpp/kernels/qwen35_primitives.cu:768-800 (validation order and messages)
+  require<Err>(qkv != nullptr, "pack_linear_delta_input qkv pointer is null");
+  require<Err>(beta != nullptr, "pack_linear_delta_input beta pointer is null");
+  require<Err>(alpha != nullptr, "pack_linear_delta_input alpha pointer is null");
+  require<Err>(gate != nullptr, "pack_linear_delta_input gate pointer is null");
+  require<Err>(packed != nullptr, "pack_linear_delta_input output pointer is null");
+  require<Err>(tokens > 0, "pack_linear_delta_input tokens must be positive");
+  require<Err>(qkv_width > 0, "pack_linear_delta_input qkv_width must be positive");
+  require<Err>(beta_width > 0, "pack_linear_delta_input beta_width must be positive");
+  require<Err>(alpha_width > 0, "pack_linear_delta_input alpha_width must be positive");
+  require<Err>(gate_width > 0, "pack_linear_delta_input gate_width must be positive");
+  require<Err>(stream != nullptr, "HIP stream is null");
+  require_dtype(dtype);
+  const std::size_t beta_end = checked_add<Err>(qkv_width, beta_width, "pack_linear_delta_input width overflow");
+  const std::size_t alpha_end = checked_add<Err>(beta_end, alpha_width, "pack_linear_delta_input width overflow");
+  const std::size_t width = checked_add<Err>(alpha_end, gate_width, "pack_linear_delta_input width overflow");
+  (void)checked_mul<Err>(tokens, width, "pack_linear_delta_input shape overflow");
+  const std::size_t es = dtype == RAFTINFER_DTYPE_F32 ? 4 : 2;
+  const std::uintptr_t addr = reinterpret_cast<std::uintptr_t>(qkv) | reinterpret_cast<std::uintptr_t>(beta) |
+                              reinterpret_cast<std::uintptr_t>(alpha) | reinterpret_cast<std::uintptr_t>(gate) |
+                              reinterpret_cast<std::uintptr_t>(packed);
+  const bool wide = (addr & 15u) == 0 && (qkv_width * es) % 16 == 0 && (beta_width * es) % 16 == 0 &&
+                    (alpha_width * es) % 16 == 0 && (gate_width * es) % 16 == 0;
+  auto grid = [](std::size_t items) {
+    return static_cast<unsigned>(std::min<std::size_t>(ceil_div_unchecked(items, 256), 65536));
+  };
+  if (wide) {
+    const std::size_t k = 16 / es;
+    pack_kernel<u32x4><<<grid(tokens * width / k), 256, 0, stream>>>(
+        static_cast<const u32x4 *>(qkv), static_cast<const u32x4 *>(beta), static_cast<const u32x4 *>(alpha),
+        static_cast<const u32x4 *>(gate), static_cast<u32x4 *>(packed), tokens, qkv_width / k,
+        beta_width / k, alpha_width / k, gate_width / k);
+  } else if (es == 4) {
+    pack_kernel<std::uint32_t><<<grid(tokens * width), 256, 0, stream>>>(
+        static_cast<const std::uint32_t *>(qkv), static_cast<const std::uint32_t *>(beta),
+        static_cast<const std::uint32_t *>(alpha), static_cast<const std::uint32_t *>(gate),
+        static_cast<std::uint32_t *>(packed), tokens, qkv_width, beta_width, alpha_width, gate_width);
+  } else {
+    pack_kernel<std::uint16_t><<<grid(tokens * width), 256, 0, stream>>>(
+        static_cast<const std::uint16_t *>(qkv), static_cast<const std::uint16_t *>(beta),
+        static_cast<const std::uint16_t *>(alpha), static_cast<const std::uint16_t *>(gate),
+        static_cast<std::uint16_t *>(packed), tokens, qkv_width, beta_width, alpha_width, gate_width);
+  }
+  check_launch<Err>("qwen35_pack_linear_delta_input");
 }
 
 void qwen35_split_query_gate_norm_rope(const void *query_gate, const void *weight, void *query,

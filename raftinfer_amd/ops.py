@@ -315,3 +315,11 @@ def qwen35_split_query_gate_norm_rope(query_gate, weight, query, gate, shape: Qk
     _call(Qwen35PrimitiveError, _lib.load().raftinfer_amd_split_query_gate_norm_rope(
         _ptr(query_gate), _ptr(weight), _ptr(query), _ptr(gate), shape.c(),
         ctypes.c_float(epsilon), dtype, weight_dtype, _stream(stream), _ptr(device_position)))
+
+
+def qwen35_pack_linear_delta_input(qkv, beta, alpha, gate, packed, tokens, qkv_width, beta_width,
+                                   alpha_width, gate_width, dtype, stream=None) -> None:
+    """cpp/kernels/qwen35_primitives.cuh:98-102."""
+    _call(Qwen35PrimitiveError, _lib.load().raftinfer_amd_pack_linear_delta_input(
+        _ptr(qkv), _ptr(beta), _ptr(alpha), _ptr(gate), _ptr(packed), tokens, qkv_width,
+        beta_width, alpha_width, gate_width, dtype, _stream(stream)))

@@ -221,3 +221,21 @@ def test_producer_validation_errors_before_launch():
         ops.qwen35_split_full_query_gate(f, f, f, 1, 1, 8, 1, stream=0)
     with pytest.raises(ops.Qwen35PrimitiveError, match="input pointer is null"):
         ops.qwen35_split_full_query_gate(None, f, f, 1, 1, 8, 1, stream=0x1234)
+
+
+def test_pack_validation_errors_before_launch():
+    # cpp/kernels/qwen35_primitives.cu:768-793: every null pointer, zero width
+    f = FakeTensor()
+    for i, msg in enumerate(["qkv pointer", "beta pointer", "alpha pointer", "gate pointer",
+                             "output pointer"]):
+        args = [f] * 5
+        args[i] = None
+        with pytest.raises(ops.Qwen35PrimitiveError, match=msg):
+            ops.qwen35_pack_linear_delta_input(*args, 1, 4, 1, 1, 4, 3, stream=0x1234)
+    for i, msg in enumerate(["qkv_width", "beta_width", "alpha_width", "gate_width"]):
+        w = [4, 1, 1, 4]
+        w[i] = 0
+        with pytest.raises(ops.Qwen35PrimitiveError, match=msg):
+            ops.qwen35_pack_linear_delta_input(f, f, f, f, f, 1, *w, 3, stream=0x1234)
+    with pytest.raises(ops.Qwen35PrimitiveError, match="width overflow"):
+        ops.qwen35_pack_linear_delta_input(f, f, f, f, f, 1, 2 ** 64 - 2, 1, 1, 4, 3, stream=0x1234)

@@ -330,3 +330,10 @@ def test_split_full_query_gate_layout():
     blocks = qg.reshape(2, heads, 2, d)
     np.testing.assert_array_equal(q, blocks[:, :, 0])
     np.testing.assert_array_equal(g, blocks[:, :, 1])
+
+
+def test_pack_linear_delta_input_layout():
+    a = np.arange(6, dtype=np.float32).reshape(2, 3)
+    b = np.array([[100.], [101.]], np.float32)
+    got = orc.pack_linear_delta_input(a, b, b + 10, a + 50)
+    np.testing.assert_array_equal(got, np.concatenate([a, b, b + 10, a + 50], axis=1))

@@ -103,3 +103,18 @@ def test_fused_split_norm_rope_equals_two_steps(gpu):
     assert torch.equal(q2, q3) and torch.equal(g1, g3)
     want = orc.qk_norm_rope(qg.reshape(T, heads, 2, d)[:, :, 0], w, rot, 77, 1e7, 1e-6)
     assert_bf16_close(from_dev(q3).reshape(T, heads, d), want, what="fused producer")
+
+
+@pytest.mark.parametrize("dt", [1, 2, 3])
+@pytest.mark.parametrize("widths", [(8192, 32, 32, 4096), (7, 3, 3, 5), (16, 8, 8, 24)])
+def test_pack_linear_delta_input_is_exact(gpu, dt, widths):
+    # cpp/tests/qwen35_cuda_primitives_test.cu (pack cases) and the model widths
+    # (qkv 2*16*128 + 32*128, beta 32, alpha 32, gate 32*128).
+    tokens = 5
+    srcs = [sequence(tokens * w, 0.011 * (k + 1), 0.1 * k).reshape(tokens, w) for k, w in enumerate(widths)]
+    dev = [to_dev(x, TDT[dt]) for x in srcs]
+    packed = torch.empty(tokens * sum(widths), device="cuda", dtype=TDT[dt])
+    ops.qwen35_pack_linear_delta_input(*dev, packed, tokens, *widths, dt)
+    torch.cuda.synchronize()
+    want = orc.pack_linear_delta_input(*[from_dev(d).reshape(tokens, -1) for d in dev])
+    np.testing.assert_array_equal(from_dev(packed).reshape(tokens, -1), want)
