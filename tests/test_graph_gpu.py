@@ -1,0 +1,108 @@
+"""Decode under HIP graph capture with a device-resident position, as the
+reference's decode graphs run it (cpp/tests/qwen35_cuda_graph_test.cu:115-183,
+cpp/kernels/qwen35_online_attention.cu:947-1014): the captured kernels read the
+position from device memory, so one graph replays every step while a captured
+kernel advances the position.  Every replay is checked against the CPU oracle,
+with eager work and synchronizations between replays.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import HKV, HQ, D, assert_bf16_close, bf16, from_dev, make_cache, normal, rng, to_dev
+from oracle import pyoracle as orc
+from raftinfer_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def test_rope_graph_follows_device_position(gpu):
+    # cpp/tests/qwen35_cuda_graph_test.cu:115-183
+    x = torch.tensor([1.0, -2.0, 0.5, 3.0], device="cuda")
+    w = torch.ones(4, device="cuda")
+    out = torch.empty(4, device="cuda")
+    pos = torch.tensor([128], device="cuda", dtype=torch.int32)
+    shape = ops.QkNormRopeShape(1, 1, 4, 2, 0, 1e4)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=gpu):
+        ops.qwen35_qk_norm_rope(x, w, out, shape, 1e-6, 1, 1, stream=gpu, device_position=pos)
+        pos.add_(1)
+    for expected_position in (128, 129, 130):
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        ref = torch.empty(4, device="cuda")
+        ops.qwen35_qk_norm_rope(x, w, ref, ops.QkNormRopeShape(1, 1, 4, 2, expected_position, 1e4),
+                                1e-6, 1, 1, stream=gpu)
+        torch.cuda.synchronize()
+        assert torch.allclose(got, ref, atol=1e-5, rtol=0)
+        want = orc.qk_norm_rope(from_dev(x).reshape(1, 1, 4), from_dev(w), 2, expected_position, 1e4, 1e-6)
+        np.testing.assert_allclose(from_dev(got), want.ravel(), atol=1e-5)
+
+
+def test_captured_decode_step_crosses_split_threshold(gpu):
+    """Producers (fused q split + norm + RoPE, k norm + RoPE) and the online
+    decode (append + single-block or split-K by the device position) captured
+    once; replayed for contexts 253 .. 260, across the 256-token threshold."""
+    max_ctx, start, steps, rot, base = 320, 252, 8, 64, 1e7
+    r = rng(2024)
+    past_k = bf16(normal(r, start, HKV, D))
+    past_v = bf16(normal(r, start, HKV, D))
+    cache = to_dev(make_cache(past_k, past_v, 1, max_ctx), torch.bfloat16)
+    wq = to_dev(bf16(normal(r, D, scale=0.2) + 1.0), torch.bfloat16)
+    wk = to_dev(bf16(normal(r, D, scale=0.2) + 1.0), torch.bfloat16)
+    qg_in = torch.empty(HQ * 2 * D, device="cuda", dtype=torch.bfloat16)
+    k_in = torch.empty(HKV * D, device="cuda", dtype=torch.bfloat16)
+    v_in = torch.empty(HKV * D, device="cuda", dtype=torch.bfloat16)
+    q_out, g_out = (torch.empty(HQ * D, device="cuda", dtype=torch.bfloat16) for _ in range(2))
+    k_out = torch.empty(HKV * D, device="cuda", dtype=torch.bfloat16)
+    out = torch.empty(HQ * D, device="cuda", dtype=torch.bfloat16)
+    pos = torch.tensor([start], device="cuda", dtype=torch.int32)
+    shape = ops.Qwen35AttentionShape(1, HQ, HKV, D, max_ctx, start)
+    plan = ops.qwen35_online_decode_plan(shape, ops.AUTO, max_ctx)
+    ws = torch.zeros(ops.qwen35_online_decode_workspace_layout(shape, plan[0])[4], device="cuda",
+                     dtype=torch.uint8)
+    qshape = ops.QkNormRopeShape(1, HQ, D, rot, 0, base)
+    kshape = ops.QkNormRopeShape(1, HKV, D, rot, 0, base)
+
+    def step():
+        ops.qwen35_split_query_gate_norm_rope(qg_in, wq, q_out, g_out, qshape, 1e-6, 3, 3,
+                                              stream=gpu, device_position=pos)
+        ops.qwen35_qk_norm_rope(k_in, wk, k_out, kshape, 1e-6, 3, 3, stream=gpu,
+                                device_position=pos)
+        ops.qwen35_online_attention_decode(q_out, k_out, v_in, g_out, out, cache, ws, shape,
+                                           ops.DTYPE_BF16, ops.CACHE_BF16, ops.HEAD_MAJOR,
+                                           plan=plan, device_position=pos, stream=gpu)
+        pos.add_(1)
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=gpu):
+        step()
+    # Capture does not run the work: the position and cache are unchanged.
+    keys, vals = list(past_k), list(past_v)
+    for s in range(steps):
+        p = start + s
+        qg = bf16(normal(r, HQ * 2 * D))
+        kn, vn = bf16(normal(r, HKV * D)), bf16(normal(r, HKV * D))
+        qg_in.copy_(to_dev(qg, torch.bfloat16))
+        k_in.copy_(to_dev(kn, torch.bfloat16))
+        v_in.copy_(to_dev(vn, torch.bfloat16))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert int(pos.item()) == p + 1
+        qg3 = qg.reshape(1, HQ, 2, D)
+        q_want = orc.qk_norm_rope(qg3[:, :, 0], from_dev(wq), rot, p, base, 1e-6)
+        k_want = orc.qk_norm_rope(kn.reshape(1, HKV, D), from_dev(wk), rot, p, base, 1e-6)
+        q_got = from_dev(q_out).reshape(HQ, D)
+        k_got = from_dev(k_out).reshape(HKV, D)
+        assert_bf16_close(q_got, q_want[0], what=f"q at position {p}")
+        assert_bf16_close(k_got, k_want[0], what=f"k at position {p}")
+        np.testing.assert_array_equal(from_dev(g_out).reshape(HQ, D), qg3[0, :, 1])
+        keys.append(k_got)
+        vals.append(vn.reshape(HKV, D))
+        want = orc.attention_core(q_got[None], np.stack(keys), np.stack(vals),
+                                  qg3[:, :, 1], p)[0]
+        assert_bf16_close(from_dev(out).reshape(HQ, D), want, what=f"decode at context {p + 1}")
+        ck = from_dev(cache)[: HKV * max_ctx * D].reshape(HKV, max_ctx, D)
+        np.testing.assert_array_equal(ck[:, p], k_got)  # the appended row is the produced k
