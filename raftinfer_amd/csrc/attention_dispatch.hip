@@ -357,7 +357,9 @@ void launch_prefill(const void *q, const void *k, const void *v, const void *g, 
   }
   if constexpr (std::is_same_v<ActT, bf16_bits> && std::is_same_v<CacheT, bf16_bits>) {
     const bool aligned = ((reinterpret_cast<std::uintptr_t>(q) |
-                           reinterpret_cast<std::uintptr_t>(cache)) & 15u) == 0;
+                           reinterpret_cast<std::uintptr_t>(cache)) & 15u) == 0 &&
+                         ((reinterpret_cast<std::uintptr_t>(g) |
+                           reinterpret_cast<std::uintptr_t>(o)) & 7u) == 0;
     if (aligned && s.query_heads == kQueryHeads && s.kv_heads == kKvHeads &&
         s.head_dim == kHeadDim) {
       amd::launch_prefill_mfma(static_cast<const bf16_bits *>(q), static_cast<const bf16_bits *>(g),

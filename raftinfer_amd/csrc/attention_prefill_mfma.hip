@@ -1,144 +1,110 @@
 // Causal gated GQA prefill attention for the Qwen3.5 signature (16 query
 // heads, 4 KV heads, head_dim 256) on gfx950 bf16 MFMA.
 //
-// Workgroup = 8 waves = one KV head x a 32-token query tile, as two key-split
-// groups of 4 waves: group g takes key tiles g, g+2, ...; wave w of a group
-// computes query head 4*kv_head + w, so every K/V tile staged in LDS serves
-// the four heads of the GQA group.  The two groups' partial (max, sum, O)
-// are merged through LDS, each group finishing one half of the head dims.  Per 32-key tile and wave:
-//   S^T = K Q^T      16 x v_mfma_f32_32x32x16_bf16 (K row-major in LDS, Q in VGPRs)
-//                    -> lane l owns query l%32 and 16 of its 32 keys, so the row
-//                    max is 15 in-register maxes plus one lane exchange;
-//   online softmax   exp2 domain; the running max only moves when a row max
-//                    grows by more than 2^8 (lazy rescaling), so the 128-register
-//                    O rescale is rare;
-//   O^T += V^T P^T   16 x v_mfma_f32_32x32x16_bf16: P^T stays in VGPRs as the B
-//                    operand; its key order is the S^T accumulator order, and
-//                    the V^T operand (V transposed in LDS) is read in that same
-//                    permuted key order, so P needs no LDS round trip.
-// The next tile's K/V loads are issued before the current tile's math.  The
-// sigmoid gate is applied in the epilogue; tiles past the causal diagonal are
-// skipped and the diagonal tile is masked per element.
+// Work split.  A workgroup owns one KV head and 8 query tokens.  The 4 query
+// heads of the GQA group x the 8 tokens are the 32 columns of one MFMA
+// operand (column c = head_in_group * 8 + token), so every K/V element read
+// serves all four heads.  The 4 waves split the key range: wave w takes the
+// 32-key tiles w, w+4, ...; at PP512 that is 256 workgroups, and the longest
+// query tile's 16 key tiles run four at a time on the CU's four SIMDs.
+//
+// Per tile and wave:
+//   staging     K and V rows go from the cache straight into the wave's own
+//               LDS tile (global_load_lds_dwordx4, two whole 512-byte rows per
+//               instruction, no VGPRs); the next tile's K is issued as soon as
+//               the current K tile has been read, its V after the current V
+//               tile.  Rows are stored as 32 16-byte chunks with chunk c at
+//               c ^ swz(row), so both operand reads below are free of bank
+//               conflicts;
+//   S^T = K Q^T 16 x v_mfma_f32_32x32x16_bf16, K rows read from LDS with
+//               ds_read_b128, Q^T held in VGPRs for the whole kernel;
+//   softmax     online in the exp2 domain; lane l owns column l % 32 and 16
+//               of the tile's keys; the reference max moves only when a
+//               column max grows by more than 2^8 (lazy rescaling);
+//   O^T += V^T P^T  16 x v_mfma_f32_32x32x16_bf16; P^T stays in VGPRs in the
+//               S^T accumulator's key order, and the V^T operand is read in
+//               that order straight from the row-major V tile with
+//               ds_read_b64_tr_b16 (lane i of a 16-lane group receives 4 keys
+//               of one dim).
+// The waves' partial (max, sum, O) are merged through LDS at the end; wave w
+// finishes dims [64w, 64w+64) and applies the sigmoid gate.
 #include "decode_scan.hpp"
 #include "prefill_mfma.hpp"
 
 namespace raftinfer::amd {
 namespace {
 
-constexpr int kQTile = 32;
-constexpr int kKTile = 32;
-constexpr int kKStride = kHeadDim + 8; // bf16 per K row in LDS (528 B)
-constexpr int kVStride = kKTile + 4;   // bf16 per transposed V row (72 B)
-constexpr float kLazyRescale = 8.0f;   // log2 units
-constexpr int kSplits = 2;             // key-split groups per workgroup
-constexpr int kThreads = 256 * kSplits;
-constexpr int kEpiStride = 128 + 4;   // fp32 per epilogue row
+constexpr int kQTok = 8;             // query tokens per workgroup
+constexpr int kKTile = 32;           // keys per tile
+constexpr int kWaves = 4;            // key-split waves per workgroup
+constexpr int kThreads = kWaves * kWave;
+constexpr int kChunks = kHeadDim / 8; // 16-byte chunks per row
+constexpr float kLazyRescale = 8.0f; // log2 units
 
-struct StageTile {
-  bf16_bits k[kKTile][kKStride];
-  bf16_bits vt[kHeadDim][kVStride];
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4v;
+
+struct WaveTile {
+  bf16_bits k[kKTile * kHeadDim];
+  bf16_bits v[kKTile * kHeadDim];
 };
-struct MainPhase {
-  // Q tile of the four heads (the B operand of S^T = K Q^T), shared by both groups.
-  bf16_bits q[kGroup][kQTile][kKStride];
-  StageTile stage[kSplits];
+struct PrefillShared {
+  union {
+    WaveTile tile[kWaves];                  // 128 KiB
+    float4 o[kWaves][8][4][kWave];          // merge: every wave's O^T, lane-major
+  };
+  float m[kWaves][kWave];
+  float l[kWaves][kWave];
 };
-union PrefillShared {
-  MainPhase main;
-  // Merge: wave w of group g leaves the half of O^T that group 1-g finishes
-  // (64 registers, lane-major), with its running max and partial sums.
-  struct {
-    float o[8][64][64];
-    float m[8][64];
-    float l[8][64];
-  } merge;
-  // Epilogue: one [query][128 dims] fp32 tile per wave.
-  float epi[8][kQTile][kEpiStride];
-};
+
+// Physical 16-byte chunk of logical chunk c in tile row r.  For 16 consecutive
+// rows the map c -> c ^ swz(r) is a different permutation of the low four bits,
+// and for 4 consecutive rows starting at a multiple of 4 it moves chunks
+// 4n..4n+3 onto 16 distinct (chunk mod 16) slots.
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+__device__ __forceinline__ int chunk_offset(int r, int c) { // in bf16 elements
+  return r * kHeadDim + ((c ^ swz(r)) << 3);
+}
 
 __device__ __forceinline__ bf16x8 lds_b128(const bf16_bits *p) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(p));
 }
 
-__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// Merge and epilogue of one key-split group; GRP selects the half of the
-// head dims it finishes.
-template <int GRP>
-__device__ __forceinline__ void prefill_tail(floatx16 (&o)[8], float m_run, float l_run,
-                                             PrefillShared &sh, const bf16_bits *__restrict__ gate,
-                                             bf16_bits *__restrict__ output, std::size_t t0,
-                                             std::size_t q_rows, std::size_t head, int wave,
-                                             int lane, int col, int half) {
-  constexpr int mine = 4 * GRP, theirs = 4 * (1 - GRP), grp = GRP;
-  // Gate loads of this lane's output rows are issued before the merge.
-  const int rq = lane >> 4;       // query of this lane within a group of 4
-  const int c8 = (lane & 15) * 8; // first dim of this lane's 8-dim chunk
-  u32x4 gv[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    // Rows past the tile's end read the last row; they are never stored.
-    const std::size_t qq = 4 * j + rq;
-    const std::size_t qr = qq < q_rows ? qq : q_rows - 1;
-    gv[j] = *reinterpret_cast<const u32x4 *>(gate + ((t0 + qr) * kQueryHeads + head) * kHeadDim +
-                                             128 * grp + c8);
-  }
-  __syncthreads(); // every wave is done with Q and the stage tiles
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) sh.merge.o[wave][nb * 16 + i][lane] = o[theirs + nb][i];
-  sh.merge.m[wave][lane] = m_run;
-  sh.merge.l[wave][lane] = l_run;
-  __syncthreads();
-  const int peer = wave ^ 4; // same head, other group
-  {
-    const float m1 = sh.merge.m[peer][lane];
-    const float mm = fmaxf(m_run, m1);
-    const float a0 = fexp2(m_run - mm);
-    const float a1 = fexp2(m1 - mm);
-    l_run = l_run * a0 + sh.merge.l[peer][lane] * a1;
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        o[mine + nb][i] = o[mine + nb][i] * a0 + sh.merge.o[peer][nb * 16 + i][lane] * a1;
-  }
-  const float l = l_run + xor32(l_run);
-  const float inv = 1.0f / l; // for query `col`
-
-  // Epilogue: each wave writes its half of O^T (register i of block nb = dim
-  // nb*32 + 8*(i/4) + half*4 + i%4 of query `col`) to its own LDS tile
-  // [query][dim], then reads it back row-major so every gate load and output
-  // store covers whole 256-byte row segments.
-  __syncthreads(); // merge buffer consumed
-  float(*ot)[kEpiStride] = sh.epi[wave];
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) {
-      const floatx16 &ob = o[mine + nb];
-      *reinterpret_cast<float4 *>(&ot[col][nb * 32 + 8 * i4 + half * 4]) =
-          make_float4(ob[4 * i4] * inv, ob[4 * i4 + 1] * inv, ob[4 * i4 + 2] * inv,
-                      ob[4 * i4 + 3] * inv);
-    }
-  wave_lds_order();
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const std::size_t qq = 4 * j + rq;
-    if (qq < q_rows) {
-      const float4 x0 = *reinterpret_cast<const float4 *>(&ot[qq][c8]);
-      const float4 x1 = *reinterpret_cast<const float4 *>(&ot[qq][c8 + 4]);
-      const u32x4 g = gv[j];
-      const u32x4 w{pack_bf16x2(x0.x * sigmoid_gate(bf16_lo(g[0])), x0.y * sigmoid_gate(bf16_hi(g[0]))),
-                    pack_bf16x2(x0.z * sigmoid_gate(bf16_lo(g[1])), x0.w * sigmoid_gate(bf16_hi(g[1]))),
-                    pack_bf16x2(x1.x * sigmoid_gate(bf16_lo(g[2])), x1.y * sigmoid_gate(bf16_hi(g[2]))),
-                    pack_bf16x2(x1.z * sigmoid_gate(bf16_lo(g[3])), x1.w * sigmoid_gate(bf16_hi(g[3])))};
-      *reinterpret_cast<u32x4 *>(output + ((t0 + qq) * kQueryHeads + head) * kHeadDim + 128 * grp +
-                                 c8) = w;
-    }
-  }
+__device__ __forceinline__ u32x2 lds_tr16(const bf16_bits *p) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v *)(p)));
 }
+
+// LDS byte address of a __shared__ object.
+template <typename T> __device__ __forceinline__ unsigned lds_address(T *p) {
+  return static_cast<unsigned>(reinterpret_cast<std::uintptr_t>(
+      (__attribute__((address_space(3))) char *)(p)));
+}
+
+// 16 bytes from base + voff (per lane) into LDS at lds + 16 * lane
+// (global_load_lds_dwordx4).  Written as asm, with the waits below issued by
+// hand: the compiler cannot tell which LDS tile such a load writes and would
+// otherwise wait for every outstanding one before each LDS read.  The kernel
+// uses no other instruction that reads M0.
+__device__ __forceinline__ void load_lds_b128(const void *base, std::uint32_t voff, unsigned lds) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds), "v"(voff), "s"(base)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
+template <int N> __device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory"); }
+
+__host__ __device__ constexpr std::size_t ceil_div_u(std::size_t n, std::size_t d) {
+  return (n + d - 1) / d;
+}
+
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
     const bf16_bits *__restrict__ query, const bf16_bits *__restrict__ gate,
@@ -148,105 +114,91 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int grp = wave >> 2;  // key-split group: tiles grp, grp + kSplits, ...
-  const int hw = wave & 3;    // query head of the GQA group
-  const int gtid = tid & 255; // thread index inside the group
-  const int col = lane & 31;  // query column of S^T / O^T
-  const int half = lane >> 5; // k-half of the operands
-  const std::size_t qtile = gridDim.x - 1 - blockIdx.x; // longest tiles first
-  const std::size_t kv_head = blockIdx.y;
-  const std::size_t head = kv_head * kGroup + hw;
-  const std::size_t t0 = qtile * kQTile;
-  const std::size_t q_rows = tokens - t0 < kQTile ? tokens - t0 : kQTile;
+  const int col = lane & 31;  // MFMA column: head_in_group * 8 + token
+  const int half = lane >> 5; // k-half of the MFMA operands
+  // XCD-aware map: the hardware deals workgroup b to XCD b % 8, and XCDs 2h,
+  // 2h+1 take KV head h, so each XCD's L2 holds one head's K/V.  Slots are
+  // dealt longest query tile first.
+  const std::size_t n_qtiles = ceil_div_u(tokens, kQTok);
+  const unsigned xcd = blockIdx.x & 7u;
+  const std::size_t slot = 2 * (blockIdx.x >> 3) + (xcd & 1u);
+  if (slot >= n_qtiles) return; // padding of an odd tile count
+  const std::size_t qtile = n_qtiles - 1 - slot;
+  const std::size_t kv_head = xcd >> 1;
+  const std::size_t t0 = qtile * kQTok;
+  const std::size_t q_rows = tokens - t0 < kQTok ? tokens - t0 : kQTok;
   const std::size_t key_end = past + t0 + q_rows;
   const std::size_t n_tiles = (key_end + kKTile - 1) / kKTile;
   const std::size_t plane = max_ctx * kKvHeads * kHeadDim;
   const float scale = kLog2e / 16.0f;
-  const std::size_t my_qpos = past + t0 + col;
-  StageTile &st = sh.main.stage[grp];
+  const int col_tok = col & (kQTok - 1);
+  const std::size_t col_row = static_cast<std::size_t>(col_tok) < q_rows ? col_tok : q_rows - 1;
+  const std::size_t col_pos = past + t0 + col_row;
+  const std::size_t col_head = kv_head * kGroup + (col >> 3);
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave); // wave index as a scalar
+  WaveTile &tile = sh.tile[wave_u];
 
-  // Q tile -> LDS: thread -> (head, query row, 64-dim quarter); rows past the
-  // tile's end repeat the last row (their outputs are never stored).
+  // Q^T operand: k-slot (kb, half, j) <-> dim 16 kb + 8 half + j.
+  bf16x8 qv[16];
+  {
+    const bf16_bits *src = query + ((t0 + col_row) * kQueryHeads + col_head) * kHeadDim + 8 * half;
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int idx = tid + kThreads * r;          // 0 .. 1023
-    const int qh = idx >> 8, qrow = (idx >> 3) & 31, seg = idx & 7;
-    const std::size_t qr = static_cast<std::size_t>(qrow) < q_rows ? qrow : q_rows - 1;
-    const bf16_bits *src = query + ((t0 + qr) * kQueryHeads + kv_head * kGroup + qh) * kHeadDim + seg * 32;
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      *reinterpret_cast<u32x4 *>(&sh.main.q[qh][qrow][seg * 32 + c * 8]) =
-          *reinterpret_cast<const u32x4 *>(src + c * 8);
+    for (int kb = 0; kb < 16; ++kb)
+      qv[kb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(src + 16 * kb));
   }
 
   floatx16 o[8];
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb) o[nb] = floatx16{};
-  float m_run = -INFINITY; // running reference max of query `col` (exp2 domain)
-  float l_run = 0.f;       // partial sum over this lane's keys
+  float m_run = -INFINITY; // reference max of column `col` (exp2 domain)
+  float l_run = 0.f;       // sum over this lane's keys, relative to m_run
 
-  // Staging map: thread -> keys 4*kg .. 4*kg+3, dims 8*db .. 8*db+7; kg varies
-  // fastest inside a wave so each load instruction covers 8 full 128-byte lines.
-  const int kg = gtid & 7;
-  const int db = gtid >> 3;
-  u32x4 kc[4], vc[4];
-  auto load_tile = [&](std::size_t k0) {
+  // Staging: load instruction i fills tile rows 2i, 2i+1 (1 KiB of LDS, lane
+  // -> row 2i + half, physical chunk `col`) straight from the cache, so the
+  // lane reads logical chunk col ^ swz(row) of its key.  Keys past key_end
+  // read row key_end - 1 (in bounds); their scores are masked.
+  const std::uint32_t row_bytes = head_major ? kHeadDim * 2 : kKvHeads * kHeadDim * 2;
+  const unsigned lds_k = lds_address(tile.k), lds_v = lds_address(tile.v);
+  auto issue = [&](const bf16_bits *plane_base, unsigned lds, std::size_t k0) {
+    const bf16_bits *base = plane_base + cache_row(head_major, k0, kv_head, max_ctx);
+    const std::size_t rows_left = key_end - k0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      // Keys past key_end read row key_end-1 (in bounds); their scores are
-      // masked to -inf, so no branch splits the batch of loads.
-      std::size_t key = k0 + 4 * kg + j;
-      key = key < key_end ? key : key_end - 1;
-      const std::size_t row = cache_row(head_major, key, kv_head, max_ctx) + 8 * db;
-      kc[j] = *reinterpret_cast<const u32x4 *>(cache + row);
-      vc[j] = *reinterpret_cast<const u32x4 *>(cache + plane + row);
+    for (int i = 0; i < 16; ++i) {
+      const int r = 2 * i + half;
+      const std::uint32_t rr = static_cast<std::size_t>(r) < rows_left ? r : rows_left - 1;
+      load_lds_b128(base, rr * row_bytes + 16u * (col ^ swz(r)), lds + 1024u * i);
     }
   };
-  // Every group runs the same number of steps (so the barriers match); a
-  // group whose tile index is past the end idles through the last step.
-  const std::size_t steps = (n_tiles + kSplits - 1) / kSplits;
-  if (static_cast<std::size_t>(grp) < n_tiles) load_tile(static_cast<std::size_t>(grp) * kKTile);
+  std::size_t t = wave_u;
+  // Issue order: K(t0) V(t0) | K(t+4) V(t+4) per tile t, so 16 loads follow
+  // K(t) when it is waited for, and 16 (or none on the last tile) follow V(t).
+  if (t < n_tiles) {
+    issue(cache, lds_k, t * kKTile);
+    issue(cache + plane, lds_v, t * kKTile);
+  }
 
-  for (std::size_t step = 0; step < steps; ++step) {
-    const std::size_t tile = step * kSplits + grp;
-    const bool active = tile < n_tiles;
-    const std::size_t k0 = tile * kKTile;
-    __syncthreads(); // previous tile fully consumed
-    if (active) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        *reinterpret_cast<u32x4 *>(&st.k[4 * kg + j][8 * db]) = kc[j];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int word = e >> 1;
-        const int shift = (e & 1) * 16;
-        const std::uint32_t v0 = (vc[0][word] >> shift) & 0xFFFFu, v1 = (vc[1][word] >> shift) & 0xFFFFu;
-        const std::uint32_t v2 = (vc[2][word] >> shift) & 0xFFFFu, v3 = (vc[3][word] >> shift) & 0xFFFFu;
-        *reinterpret_cast<u32x2 *>(&st.vt[8 * db + e][4 * kg]) = u32x2{v0 | (v1 << 16), v2 | (v3 << 16)};
-      }
-    }
-    __syncthreads();
-    if (!active) continue;
-    if (tile + kSplits < n_tiles) load_tile(k0 + kSplits * kKTile); // prefetch the next tile
-
-    // S^T = K Q^T: rows = keys, column = query `col`.
+  for (; t < n_tiles; t += kWaves) {
+    const std::size_t k0 = t * kKTile;
+    const bool more = t + kWaves < n_tiles;
+    wait_vm<16>(); // K(t) has landed; V(t) may still be in flight
+    // S^T = K Q^T: A row = key `col` of the tile (lane & 31), k-half `half`.
     floatx16 s = floatx16{};
 #pragma unroll
     for (int kb = 0; kb < 16; ++kb)
-      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_b128(&st.k[col][kb * 16 + half * 8]),
-                                                  lds_b128(&sh.main.q[hw][col][kb * 16 + half * 8]), s,
-                                                  0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_b128(&tile.k[chunk_offset(col, 2 * kb + half)]),
+                                                  qv[kb], s, 0, 0, 0);
+    wait_lgkm0(); // the K tile has been read
+    if (more) issue(cache, lds_k, k0 + kWaves * kKTile);
 
-    // Key of accumulator register i: 8*(i/4) + half*4 + i%4.
+    // Key of accumulator register i: 8 (i / 4) + 4 half + i % 4.
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const std::size_t key = k0 + (i >> 2) * 8 + half * 4 + (i & 3);
-      s[i] = (key > my_qpos || key >= key_end) ? -INFINITY : s[i] * scale;
+      s[i] = key > col_pos ? -INFINITY : s[i] * scale;
       mx = fmaxf(mx, s[i]);
     }
     mx = max_xor32(mx);
-    // Lazy rescale: move the reference max only when it grows by > 2^8.
     const bool grow = mx > m_run + kLazyRescale;
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {
       const float m_new = grow ? mx : m_run;
@@ -258,7 +210,7 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
         for (int i = 0; i < 16; ++i) o[nb][i] *= sc;
       m_run = m_new;
     }
-    u32x4 pw[2];
+    bf16x8 pw[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       float p[8];
@@ -267,37 +219,99 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
         p[j] = fexp2(s[8 * kb + j] - m_run);
         l_run += p[j];
       }
-      pw[kb] = u32x4{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
-                     pack_bf16x2(p[6], p[7])};
+      pw[kb] = __builtin_bit_cast(bf16x8, u32x4{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
+                                                pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])});
     }
-    // O^T += V^T P^T.  k-slot (kb, j) of this lane <-> key
-    // 16kb + 4*half + j (j < 4) and 16kb + 8 + 4*half + (j-4) (j >= 4).
+
+    if (more) wait_vm<16>(); else wait_vm<0>(); // V(t) has landed
+    // O^T += V^T P^T.  k-slot (kb, half, j) <-> key 16 kb + 4 half + j (j < 4)
+    // and 16 kb + 8 + 4 half + (j - 4) (j >= 4), the P^T register order.  A
+    // row (dim) 32 nb + 16 (g & 1) + r of 16-lane group g: source lane r of
+    // the transposed read supplies dims 4 (r & 3) .. +3 of key (r >> 2).
+    {
+      const int g = lane >> 4, r = lane & 15;
+      const int trow = 4 * half + (r >> 2);
+      const int dsub = 16 * (g & 1) + 4 * (r & 3); // dim offset inside the 32-dim block
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
+      for (int nb = 0; nb < 8; ++nb) {
+        const int d = 32 * nb + dsub;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const bf16_bits *vrow = &st.vt[nb * 32 + col][16 * kb + 4 * half];
-        const u32x2 lo = *reinterpret_cast<const u32x2 *>(vrow);
-        const u32x2 hi = *reinterpret_cast<const u32x2 *>(vrow + 8);
-        const bf16x8 a = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-        o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8, pw[kb]),
-                                                        o[nb], 0, 0, 0);
+        for (int kb = 0; kb < 2; ++kb) {
+          const int r0 = 16 * kb + trow, r1 = r0 + 8;
+          const u32x2 lo = lds_tr16(&tile.v[chunk_offset(r0, d >> 3) + (d & 7)]);
+          const u32x2 hi = lds_tr16(&tile.v[chunk_offset(r1, d >> 3) + (d & 7)]);
+          const bf16x8 a = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+          o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pw[kb], o[nb], 0, 0, 0);
+        }
       }
     }
+    wait_lgkm0(); // the V tile has been read
+    if (more) issue(cache + plane, lds_v, k0 + kWaves * kKTile);
   }
 
-  // Each group finishes one half of the dims (group g: dims 128g .. 128g+127,
-  // O^T blocks 4g .. 4g+3) for its head: it takes the other group's partial
-  // of that half, M = max(m_own, m_other), O = O_own 2^(m_own-M) +
-  // O_other 2^(m_other-M), likewise l.  A group that saw no key has m = -inf
-  // (weight 0); group 0 always saw key 0.
-  // Register indices must be compile-time constants (a run-time index into
-  // o[] would move the accumulators to scratch), so each group runs its own
-  // instantiation of the tail.
-  if (grp == 0)
-    prefill_tail<0>(o, m_run, l_run, sh, gate, output, t0, q_rows, head, wave, lane, col, half);
-  else
-    prefill_tail<1>(o, m_run, l_run, sh, gate, output, t0, q_rows, head, wave, lane, col, half);
+  // Gate loads for this wave's output quarter are issued before the merge.
+  // Register i of O^T block nb holds dim 32 nb + 8 (i / 4) + 4 half + i % 4.
+  const bool col_live = static_cast<std::size_t>(col_tok) < q_rows;
+  const std::size_t out_row = ((t0 + col_row) * kQueryHeads + col_head) * kHeadDim;
+  u32x2 gv[2][4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4)
+      gv[j][i4] = *reinterpret_cast<const u32x2 *>(gate + out_row + 32 * (2 * wave + j) + 8 * i4 +
+                                                   4 * half);
+
+  __syncthreads(); // every wave is done with its tile
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4)
+      sh.o[wave][nb][i4][lane] =
+          make_float4(o[nb][4 * i4], o[nb][4 * i4 + 1], o[nb][4 * i4 + 2], o[nb][4 * i4 + 3]);
+  sh.m[wave][lane] = m_run;
+  sh.l[wave][lane] = l_run;
+  __syncthreads();
+
+  // Wave `wave` finishes O^T blocks 2 wave and 2 wave + 1.  A wave that saw no
+  // key has m = -inf (weight 0); wave 0 always saw key 0.
+  float mw[kWaves], mm = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    mw[w] = sh.m[w][lane];
+    mm = fmaxf(mm, mw[w]);
+  }
+  float lsum = 0.f;
+  floatx16 f[2] = {floatx16{}, floatx16{}};
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const float a = fexp2(mw[w] - mm);
+    lsum += a * sh.l[w][lane];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const float4 x = sh.o[w][2 * wave + j][i4][lane];
+        f[j][4 * i4] += a * x.x;
+        f[j][4 * i4 + 1] += a * x.y;
+        f[j][4 * i4 + 2] += a * x.z;
+        f[j][4 * i4 + 3] += a * x.w;
+      }
+  }
+  const float inv = 1.0f / (lsum + xor32(lsum));
+  if (col_live) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const u32x2 g = gv[j][i4];
+        const floatx16 &x = f[j];
+        const u32x2 w{pack_bf16x2(x[4 * i4] * inv * sigmoid_gate(bf16_lo(g[0])),
+                                  x[4 * i4 + 1] * inv * sigmoid_gate(bf16_hi(g[0]))),
+                      pack_bf16x2(x[4 * i4 + 2] * inv * sigmoid_gate(bf16_lo(g[1])),
+                                  x[4 * i4 + 3] * inv * sigmoid_gate(bf16_hi(g[1])))};
+        *reinterpret_cast<u32x2 *>(output + out_row + 32 * (2 * wave + j) + 8 * i4 + 4 * half) = w;
+      }
+  }
 }
 
 } // namespace
@@ -305,7 +319,8 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
 void launch_prefill_mfma(const bf16_bits *q, const bf16_bits *gate, bf16_bits *out,
                          const bf16_bits *cache, std::size_t tokens, std::size_t max_ctx,
                          std::size_t past, bool head_major, hipStream_t stream) {
-  const dim3 grid{static_cast<unsigned>(ceil_div_unchecked(tokens, kQTile)), kKvHeads, 1};
+  // 8 workgroups (one per XCD) per pair of query tiles.
+  const unsigned grid = static_cast<unsigned>(8 * ceil_div_unchecked(ceil_div_unchecked(tokens, kQTok), 2));
   prefill_mfma_kernel<<<grid, kThreads, 0, stream>>>(q, gate, out, cache, tokens, max_ctx, past,
                                                 head_major);
 }
