@@ -51,17 +51,18 @@ struct WaveTile {
 struct PrefillShared {
   union {
     WaveTile tile[kWaves];                  // 128 KiB
-    float4 o[kWaves][8][4][kWave];          // merge: every wave's O^T, lane-major
+    // merge: [finishing wave][source wave][block][register quad][lane]
+    float4 o[kWaves][kWaves][2][4][kWave];
   };
+  bf16_bits q[32 * kHeadDim]; // Q^T operand rows (one per column), swizzled like K
   float m[kWaves][kWave];
   float l[kWaves][kWave];
 };
 
-// Physical 16-byte chunk of logical chunk c in tile row r.  For 16 consecutive
-// rows the map c -> c ^ swz(r) is a different permutation of the low four bits,
-// and for 4 consecutive rows starting at a multiple of 4 it moves chunks
-// 4n..4n+3 onto 16 distinct (chunk mod 16) slots.
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+// Physical 16-byte chunk of logical chunk c in tile row r: c ^ (r & 7).  An
+// 8-lane group of a ds_read_b128 (8 rows, one logical chunk) and a 16-lane
+// group of a ds_read_b64_tr_b16 (4 rows x 4 chunks) then hit distinct banks.
+__device__ __forceinline__ int swz(int r) { return r & 7; }
 
 __device__ __forceinline__ int chunk_offset(int r, int c) { // in bf16 elements
   return r * kHeadDim + ((c ^ swz(r)) << 3);
@@ -104,12 +105,36 @@ __host__ __device__ constexpr std::size_t ceil_div_u(std::size_t n, std::size_t 
   return (n + d - 1) / d;
 }
 
+// o += a * b (v_mfma_f32_32x32x16_bf16) with the accumulator pinned to AGPRs.
+// The compiler would otherwise move all 128 accumulator registers between
+// AGPRs and VGPRs around every tile because of the (rare) rescale code.  The
+// s_nop covers the VALU-write -> MFMA-read hazard of the operands, which the
+// hazard recognizer does not see through asm.
+__device__ __forceinline__ void mfma_acc_agpr(floatx16 &o, bf16x8 a, bf16x8 b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(o) : "v"(a), "v"(b));
+}
+// o *= s for an AGPR-resident accumulator.  The empty asm statements pin the
+// copy to VGPRs inside this (rare) rescale path; without them the compiler
+// hoists the AGPR -> VGPR copies of all accumulators onto every tile.
+__device__ __forceinline__ void scale_agpr(floatx16 &o, float s) {
+  floatx16 x = o;
+  asm volatile("" : "+v"(x));
+#pragma unroll
+  for (int i = 0; i < 16; ++i) x[i] *= s;
+  asm volatile("" : "+v"(x));
+  o = x;
+}
+// Wait states after the last such MFMA before VALU code reads its result.
+__device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory"); }
+
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+template <bool HeadMajor>
 __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
     const bf16_bits *__restrict__ query, const bf16_bits *__restrict__ gate,
     bf16_bits *__restrict__ output, const bf16_bits *__restrict__ cache, std::size_t tokens,
-    std::size_t max_ctx, std::size_t past, bool head_major) {
+    std::size_t max_ctx, std::size_t past) {
+  constexpr bool head_major = HeadMajor;
   __shared__ PrefillShared sh;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -138,15 +163,6 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
   const int wave_u = __builtin_amdgcn_readfirstlane(wave); // wave index as a scalar
   WaveTile &tile = sh.tile[wave_u];
 
-  // Q^T operand: k-slot (kb, half, j) <-> dim 16 kb + 8 half + j.
-  bf16x8 qv[16];
-  {
-    const bf16_bits *src = query + ((t0 + col_row) * kQueryHeads + col_head) * kHeadDim + 8 * half;
-#pragma unroll
-    for (int kb = 0; kb < 16; ++kb)
-      qv[kb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(src + 16 * kb));
-  }
-
   floatx16 o[8];
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb) o[nb] = floatx16{};
@@ -157,18 +173,72 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
   // -> row 2i + half, physical chunk `col`) straight from the cache, so the
   // lane reads logical chunk col ^ swz(row) of its key.  Keys past key_end
   // read row key_end - 1 (in bounds); their scores are masked.
-  const std::uint32_t row_bytes = head_major ? kHeadDim * 2 : kKvHeads * kHeadDim * 2;
+  constexpr std::uint32_t row_bytes = head_major ? kHeadDim * 2 : kKvHeads * kHeadDim * 2;
   const unsigned lds_k = lds_address(tile.k), lds_v = lds_address(tile.v);
+  // Lane offsets of a whole tile: row 2i + half, chunk col ^ swz(row); swz
+  // repeats every 8 rows, so four per-lane values serve all 16 instructions.
+  std::uint32_t voff_full[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    voff_full[i] = (2 * i + half) * row_bytes + 16u * (col ^ swz(2 * i + half));
   auto issue = [&](const bf16_bits *plane_base, unsigned lds, std::size_t k0) {
     const bf16_bits *base = plane_base + cache_row(head_major, k0, kv_head, max_ctx);
     const std::size_t rows_left = key_end - k0;
+    if (rows_left >= kKTile) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = 2 * i + half;
-      const std::uint32_t rr = static_cast<std::size_t>(r) < rows_left ? r : rows_left - 1;
-      load_lds_b128(base, rr * row_bytes + 16u * (col ^ swz(r)), lds + 1024u * i);
+      for (int i = 0; i < 16; ++i)
+        load_lds_b128(base, voff_full[i & 3] + 8 * (i >> 2) * row_bytes, lds + 1024u * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = 2 * i + half;
+        const int last = static_cast<int>(rows_left) - 1;
+        const std::uint32_t rr = r < last ? r : last;
+        load_lds_b128(base, rr * row_bytes + 16u * (col ^ swz(r)), lds + 1024u * i);
+      }
     }
   };
+  int k_base[4], v_base[2]; // element offsets inside a tile
+#pragma unroll
+  for (int j = 0; j < 4; ++j) k_base[j] = chunk_offset(col, 2 * j + half);
+  {
+    const int g = lane >> 4, r = lane & 15;
+    const int trow = 4 * half + (r >> 2);
+    const int dsub = 16 * (g & 1) + 4 * (r & 3); // dim offset inside a 32-dim block
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int d = 32 * j + dsub;
+      v_base[j] = chunk_offset(trow, d >> 3) + (d & 7);
+    }
+  }
+  // Gate loads for this wave's output quarter (dims 64 wave .. +63) go out
+  // first: they are needed only in the epilogue, so the whole tile loop hides
+  // their latency.
+  // Register i of O^T block nb holds dim 32 nb + 8 (i / 4) + 4 half + i % 4.
+  const bool col_live = static_cast<std::size_t>(col_tok) < q_rows;
+  const std::size_t out_row = ((t0 + col_row) * kQueryHeads + col_head) * kHeadDim;
+  u32x2 gv[2][4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4)
+      gv[j][i4] = *reinterpret_cast<const u32x2 *>(gate + out_row + 32 * (2 * wave + j) + 8 * i4 +
+                                                   4 * half);
+  // Q tile -> LDS, row = column c (token c % 8 of head 4 kv + c / 8), in the
+  // K tile's chunk order; wave w loads rows 8w .. 8w+7 (4 instructions).
+  {
+    const unsigned lq = lds_address(sh.q);
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const int i = 4 * wave_u + ii;
+      const int r = 2 * i + half; // column of this lane's row
+      const int rt = r & (kQTok - 1);
+      const std::size_t rrow = static_cast<std::size_t>(rt) < q_rows ? rt : q_rows - 1;
+      const std::uint32_t voff = static_cast<std::uint32_t>(rrow * kQueryHeads + (r >> 3)) * (kHeadDim * 2) +
+                                 16u * (col ^ swz(r));
+      load_lds_b128(query + (t0 * kQueryHeads + kv_head * kGroup) * kHeadDim, voff, lq + 1024u * i);
+    }
+  }
   std::size_t t = wave_u;
   // Issue order: K(t0) V(t0) | K(t+4) V(t+4) per tile t, so 16 loads follow
   // K(t) when it is waited for, and 16 (or none on the last tile) follow V(t).
@@ -177,46 +247,63 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
     issue(cache + plane, lds_v, t * kKTile);
   }
 
+  if (t < n_tiles) wait_vm<32>(); else wait_vm<0>(); // this wave's Q rows have landed
+  __syncthreads(); // ... and every other wave's
   for (; t < n_tiles; t += kWaves) {
     const std::size_t k0 = t * kKTile;
     const bool more = t + kWaves < n_tiles;
     wait_vm<16>(); // K(t) has landed; V(t) may still be in flight
     // S^T = K Q^T: A row = key `col` of the tile (lane & 31), k-half `half`.
+    // Chunk 2 kb + half of row `col` sits at (2 (kb & 3) + half) ^ (col & 7)
+    // + 8 (kb >> 2): four lane bases plus constant offsets.
     floatx16 s = floatx16{};
 #pragma unroll
     for (int kb = 0; kb < 16; ++kb)
-      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_b128(&tile.k[chunk_offset(col, 2 * kb + half)]),
-                                                  qv[kb], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_b128(tile.k + k_base[kb & 3] + 64 * (kb >> 2)),
+                                                  lds_b128(sh.q + k_base[kb & 3] + 64 * (kb >> 2)),
+                                                  s, 0, 0, 0);
     wait_lgkm0(); // the K tile has been read
     if (more) issue(cache, lds_k, k0 + kWaves * kKTile);
 
-    // Key of accumulator register i: 8 (i / 4) + 4 half + i % 4.
+    // Key of accumulator register i: k0 + 8 (i / 4) + 4 half + i % 4.  Only
+    // a tile that reaches past the tile's first query position is masked.
     float mx = -INFINITY;
+    if (k0 + kKTile - 1 > past + t0) {
+      const std::ptrdiff_t rel_pos = static_cast<std::ptrdiff_t>(col_pos - k0) - 4 * half;
+      const int lim = rel_pos < -1 ? -1 : (rel_pos > kKTile ? kKTile : static_cast<int>(rel_pos));
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const std::size_t key = k0 + (i >> 2) * 8 + half * 4 + (i & 3);
-      s[i] = key > col_pos ? -INFINITY : s[i] * scale;
-      mx = fmaxf(mx, s[i]);
+      for (int i = 0; i < 16; ++i) {
+        s[i] = (i >> 2) * 8 + (i & 3) > lim ? -INFINITY : s[i] * scale;
+        mx = fmaxf(mx, s[i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        s[i] *= scale;
+        mx = fmaxf(mx, s[i]);
+      }
     }
     mx = max_xor32(mx);
     const bool grow = mx > m_run + kLazyRescale;
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      // Lanes that do not grow keep their scale (1, also when m is still -inf).
       const float m_new = grow ? mx : m_run;
-      const float sc = fexp2(m_run - m_new); // -inf -> 0 on the first tile
+      const float sc = grow ? fexp2(m_run - mx) : 1.0f; // -inf -> 0 on a first tile
       l_run *= sc;
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[nb][i] *= sc;
+      for (int nb = 0; nb < 8; ++nb) scale_agpr(o[nb], sc);
       m_run = m_new;
     }
+    // A column whose keys so far are all masked keeps m = -inf; its
+    // probabilities are exp2(-inf - 0) = 0 rather than exp2(-inf + inf).
+    const float m_ref = m_run == -INFINITY ? 0.f : m_run;
     bf16x8 pw[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       float p[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        p[j] = fexp2(s[8 * kb + j] - m_run);
+        p[j] = fexp2(s[8 * kb + j] - m_ref);
         l_run += p[j];
       }
       pw[kb] = __builtin_bit_cast(bf16x8, u32x4{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
@@ -228,52 +315,49 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
     // and 16 kb + 8 + 4 half + (j - 4) (j >= 4), the P^T register order.  A
     // row (dim) 32 nb + 16 (g & 1) + r of 16-lane group g: source lane r of
     // the transposed read supplies dims 4 (r & 3) .. +3 of key (r >> 2).
+    // Row 16 kb + trow (+ 8) and dim 32 nb + dsub: the swizzle key is trow & 7
+    // for every row read, so two lane bases (nb & 1) plus constant offsets
+    // (rows 16 kb (+8), chunk 8 (nb >> 1)) cover all 32 reads.
     {
-      const int g = lane >> 4, r = lane & 15;
-      const int trow = 4 * half + (r >> 2);
-      const int dsub = 16 * (g & 1) + 4 * (r & 3); // dim offset inside the 32-dim block
 #pragma unroll
       for (int nb = 0; nb < 8; ++nb) {
-        const int d = 32 * nb + dsub;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
-          const int r0 = 16 * kb + trow, r1 = r0 + 8;
-          const u32x2 lo = lds_tr16(&tile.v[chunk_offset(r0, d >> 3) + (d & 7)]);
-          const u32x2 hi = lds_tr16(&tile.v[chunk_offset(r1, d >> 3) + (d & 7)]);
+          const bf16_bits *v0 = tile.v + v_base[nb & 1] + 64 * (nb >> 1) + kHeadDim * 16 * kb;
+          const u32x2 lo = lds_tr16(v0);
+          const u32x2 hi = lds_tr16(v0 + kHeadDim * 8);
           const bf16x8 a = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-          o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pw[kb], o[nb], 0, 0, 0);
+          mfma_acc_agpr(o[nb], a, pw[kb]);
         }
       }
+      mfma_drain(); // the accumulators may be read by VALU code below
     }
     wait_lgkm0(); // the V tile has been read
     if (more) issue(cache + plane, lds_v, k0 + kWaves * kKTile);
   }
 
-  // Gate loads for this wave's output quarter are issued before the merge.
-  // Register i of O^T block nb holds dim 32 nb + 8 (i / 4) + 4 half + i % 4.
-  const bool col_live = static_cast<std::size_t>(col_tok) < q_rows;
-  const std::size_t out_row = ((t0 + col_row) * kQueryHeads + col_head) * kHeadDim;
-  u32x2 gv[2][4];
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4)
-      gv[j][i4] = *reinterpret_cast<const u32x2 *>(gate + out_row + 32 * (2 * wave + j) + 8 * i4 +
-                                                   4 * half);
 
   __syncthreads(); // every wave is done with its tile
+  // Wave w finishes O^T blocks 2w, 2w+1 (dims 64w .. 64w+63): it hands the
+  // other three quarters over through LDS and keeps its own in registers.
+  // (The quarter loop is unrolled so that every register index is a
+  // compile-time constant.)
 #pragma unroll
-  for (int nb = 0; nb < 8; ++nb)
+  for (int q = 0; q < kWaves; ++q) {
+    if (q == wave) continue;
 #pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4)
-      sh.o[wave][nb][i4][lane] =
-          make_float4(o[nb][4 * i4], o[nb][4 * i4 + 1], o[nb][4 * i4 + 2], o[nb][4 * i4 + 3]);
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const floatx16 &x = o[2 * q + j];
+        sh.o[q][wave][j][i4][lane] = make_float4(x[4 * i4], x[4 * i4 + 1], x[4 * i4 + 2], x[4 * i4 + 3]);
+      }
+  }
   sh.m[wave][lane] = m_run;
   sh.l[wave][lane] = l_run;
   __syncthreads();
 
-  // Wave `wave` finishes O^T blocks 2 wave and 2 wave + 1.  A wave that saw no
-  // key has m = -inf (weight 0); wave 0 always saw key 0.
+  // A wave that saw no key has m = -inf and weight 0; wave 0 always saw key 0.
   float mw[kWaves], mm = -INFINITY;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
@@ -281,16 +365,26 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
     mm = fmaxf(mm, mw[w]);
   }
   float lsum = 0.f;
-  floatx16 f[2] = {floatx16{}, floatx16{}};
+  floatx16 f[2];
+#pragma unroll
+  for (int q = 0; q < kWaves; ++q) {
+    if (q != wave) continue;
+    const float a = fexp2(m_run - mm);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) f[j][i] = a * o[2 * q + j][i];
+  }
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
     const float a = fexp2(mw[w] - mm);
     lsum += a * sh.l[w][lane];
+    if (w == wave) continue;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
-        const float4 x = sh.o[w][2 * wave + j][i4][lane];
+        const float4 x = sh.o[wave][w][j][i4][lane];
         f[j][4 * i4] += a * x.x;
         f[j][4 * i4 + 1] += a * x.y;
         f[j][4 * i4 + 2] += a * x.z;
@@ -321,8 +415,10 @@ void launch_prefill_mfma(const bf16_bits *q, const bf16_bits *gate, bf16_bits *o
                          std::size_t past, bool head_major, hipStream_t stream) {
   // 8 workgroups (one per XCD) per pair of query tiles.
   const unsigned grid = static_cast<unsigned>(8 * ceil_div_unchecked(ceil_div_unchecked(tokens, kQTok), 2));
-  prefill_mfma_kernel<<<grid, kThreads, 0, stream>>>(q, gate, out, cache, tokens, max_ctx, past,
-                                                head_major);
+  if (head_major)
+    prefill_mfma_kernel<true><<<grid, kThreads, 0, stream>>>(q, gate, out, cache, tokens, max_ctx, past);
+  else
+    prefill_mfma_kernel<false><<<grid, kThreads, 0, stream>>>(q, gate, out, cache, tokens, max_ctx, past);
 }
 
 } // namespace raftinfer::amd

@@ -80,6 +80,16 @@ def test_decode_cfg1_single_block_ctx512(gpu):
     assert np.array_equal(ck, keys) and np.array_equal(cv, vals)  # append is bit-exact
 
 
+@pytest.mark.parametrize("T,past", [(8, 30), (3, 62), (5, 91), (9, 123)])
+def test_prefill_mfma_key_tile_past_first_query(gpu, T, past):
+    # Regression: a key-split wave whose first key tile starts after some
+    # query positions of the workgroup sees only masked scores for those
+    # columns; their probabilities must be 0, not exp2(-inf + inf) = NaN.
+    out, expect, *_ = run_prefill(3, 1, 1, T, HQ, HKV, D, past, seed=T * 1000 + past)
+    assert np.isfinite(out).all()
+    assert_bf16_close(out, bf16(expect), what=f"prefill T={T} past={past}")
+
+
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("act,cdt", [(1, 0), (1, 1), (3, 0), (3, 1)])
 @pytest.mark.parametrize("ctx", [32, 128, 512])
