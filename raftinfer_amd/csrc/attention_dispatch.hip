@@ -349,22 +349,27 @@ void launch_prefill(const void *q, const void *k, const void *v, const void *g, 
   const bool head_major = layout == Qwen35KvCacheLayout::head_major;
   const std::size_t kv_elements = s.tokens * s.kv_heads * s.head_dim;
   const int append_grid = static_cast<int>(ceil_div_unchecked(kv_elements, kBlockSize));
-  if (!kernel_only) {
+  bool mfma = false, fused = false;
+  if constexpr (std::is_same_v<ActT, bf16_bits> && std::is_same_v<CacheT, bf16_bits>) {
+    const auto bits = [](const void *p) { return reinterpret_cast<std::uintptr_t>(p); };
+    mfma = ((bits(q) | bits(cache)) & 15u) == 0 && ((bits(g) | bits(o)) & 7u) == 0 &&
+           s.query_heads == kQueryHeads && s.kv_heads == kKvHeads && s.head_dim == kHeadDim;
+    // A prompt with no past reads its keys straight from key/value and
+    // appends them inside the attention kernel.
+    fused = mfma && s.past_tokens == 0 && ((bits(k) | bits(v)) & 15u) == 0;
+  }
+  if (!kernel_only && !fused) {
     append_prefill_kernel<ActT, CacheT><<<append_grid, kBlockSize, 0, stream>>>(
         static_cast<const ActT *>(k), static_cast<const ActT *>(v), static_cast<CacheT *>(cache),
         s.tokens, s.kv_heads, s.head_dim, s.max_context_tokens, s.past_tokens, head_major);
     check_launch<Err>("qwen35_online_attention_append_cache");
   }
-  if constexpr (std::is_same_v<ActT, bf16_bits> && std::is_same_v<CacheT, bf16_bits>) {
-    const bool aligned = ((reinterpret_cast<std::uintptr_t>(q) |
-                           reinterpret_cast<std::uintptr_t>(cache)) & 15u) == 0 &&
-                         ((reinterpret_cast<std::uintptr_t>(g) |
-                           reinterpret_cast<std::uintptr_t>(o)) & 7u) == 0;
-    if (aligned && s.query_heads == kQueryHeads && s.kv_heads == kKvHeads &&
-        s.head_dim == kHeadDim) {
-      amd::launch_prefill_mfma(static_cast<const bf16_bits *>(q), static_cast<const bf16_bits *>(g),
-                               static_cast<bf16_bits *>(o), static_cast<const bf16_bits *>(cache),
-                               s.tokens, s.max_context_tokens, s.past_tokens, head_major, stream);
+  if (mfma) {
+    if constexpr (std::is_same_v<ActT, bf16_bits> && std::is_same_v<CacheT, bf16_bits>) {
+      amd::launch_prefill_mfma(static_cast<const bf16_bits *>(q), static_cast<const bf16_bits *>(k),
+                               static_cast<const bf16_bits *>(v), static_cast<const bf16_bits *>(g),
+                               static_cast<bf16_bits *>(o), static_cast<bf16_bits *>(cache), s.tokens,
+                               s.max_context_tokens, s.past_tokens, head_major, fused, stream);
       check_launch<Err>("qwen35_online_attention_prefill_gfx950_mfma_hd256");
       return;
     }

@@ -129,10 +129,15 @@ __device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\
 
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-template <bool HeadMajor>
+// FromInput: past == 0 and every key is read from the key/value inputs
+// ([tokens][4][256]); the workgroup also writes its own tokens' rows into the
+// cache (the append), so no separate append kernel runs.  Otherwise keys are
+// read from the cache, which already holds them.
+template <bool HeadMajor, bool FromInput>
 __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
-    const bf16_bits *__restrict__ query, const bf16_bits *__restrict__ gate,
-    bf16_bits *__restrict__ output, const bf16_bits *__restrict__ cache, std::size_t tokens,
+    const bf16_bits *__restrict__ query, const bf16_bits *__restrict__ key_in,
+    const bf16_bits *__restrict__ value_in, const bf16_bits *__restrict__ gate,
+    bf16_bits *__restrict__ output, bf16_bits *__restrict__ cache, std::size_t tokens,
     std::size_t max_ctx, std::size_t past) {
   constexpr bool head_major = HeadMajor;
   __shared__ PrefillShared sh;
@@ -173,7 +178,11 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
   // -> row 2i + half, physical chunk `col`) straight from the cache, so the
   // lane reads logical chunk col ^ swz(row) of its key.  Keys past key_end
   // read row key_end - 1 (in bounds); their scores are masked.
-  constexpr std::uint32_t row_bytes = head_major ? kHeadDim * 2 : kKvHeads * kHeadDim * 2;
+  constexpr std::uint32_t row_bytes = head_major && !FromInput ? kHeadDim * 2 : kKvHeads * kHeadDim * 2;
+  // Row 0 of this KV head in the K and V sources.
+  const bf16_bits *k_src = FromInput ? key_in + kv_head * kHeadDim
+                                     : cache + cache_row(head_major, 0, kv_head, max_ctx);
+  const bf16_bits *v_src = FromInput ? value_in + kv_head * kHeadDim : k_src + plane;
   const unsigned lds_k = lds_address(tile.k), lds_v = lds_address(tile.v);
   // Lane offsets of a whole tile: row 2i + half, chunk col ^ swz(row); swz
   // repeats every 8 rows, so four per-lane values serve all 16 instructions.
@@ -182,7 +191,7 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
   for (int i = 0; i < 4; ++i)
     voff_full[i] = (2 * i + half) * row_bytes + 16u * (col ^ swz(2 * i + half));
   auto issue = [&](const bf16_bits *plane_base, unsigned lds, std::size_t k0) {
-    const bf16_bits *base = plane_base + cache_row(head_major, k0, kv_head, max_ctx);
+    const bf16_bits *base = plane_base + k0 * (row_bytes / 2);
     const std::size_t rows_left = key_end - k0;
     if (rows_left >= kKTile) {
 #pragma unroll
@@ -209,6 +218,19 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
     for (int j = 0; j < 2; ++j) {
       const int d = 32 * j + dsub;
       v_base[j] = chunk_offset(trow, d >> 3) + (d & 7);
+    }
+  }
+  // Append (FromInput): thread -> two 16-byte pieces of this workgroup's K/V
+  // rows (2 planes x 8 tokens x 32 pieces); loaded now, stored at the end.
+  u32x4 app[2];
+  if constexpr (FromInput) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int idx = tid + kThreads * j; // 0 .. 511
+      const int pl = idx >> 8, tok = (idx >> 5) & 7, piece = idx & 31;
+      const std::size_t tt = static_cast<std::size_t>(tok) < q_rows ? tok : q_rows - 1;
+      const bf16_bits *src = (pl ? value_in : key_in) + ((t0 + tt) * kKvHeads + kv_head) * kHeadDim;
+      app[j] = *reinterpret_cast<const u32x4 *>(src + 8 * piece);
     }
   }
   // Gate loads for this wave's output quarter (dims 64 wave .. +63) go out
@@ -243,8 +265,8 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
   // Issue order: K(t0) V(t0) | K(t+4) V(t+4) per tile t, so 16 loads follow
   // K(t) when it is waited for, and 16 (or none on the last tile) follow V(t).
   if (t < n_tiles) {
-    issue(cache, lds_k, t * kKTile);
-    issue(cache + plane, lds_v, t * kKTile);
+    issue(k_src, lds_k, t * kKTile);
+    issue(v_src, lds_v, t * kKTile);
   }
 
   if (t < n_tiles) wait_vm<32>(); else wait_vm<0>(); // this wave's Q rows have landed
@@ -263,7 +285,7 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
                                                   lds_b128(sh.q + k_base[kb & 3] + 64 * (kb >> 2)),
                                                   s, 0, 0, 0);
     wait_lgkm0(); // the K tile has been read
-    if (more) issue(cache, lds_k, k0 + kWaves * kKTile);
+    if (more) issue(k_src, lds_k, k0 + kWaves * kKTile);
 
     // Key of accumulator register i: k0 + 8 (i / 4) + 4 half + i % 4.  Only
     // a tile that reaches past the tile's first query position is masked.
@@ -333,7 +355,7 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
       mfma_drain(); // the accumulators may be read by VALU code below
     }
     wait_lgkm0(); // the V tile has been read
-    if (more) issue(cache + plane, lds_v, k0 + kWaves * kKTile);
+    if (more) issue(v_src, lds_v, k0 + kWaves * kKTile);
   }
 
 
@@ -406,19 +428,40 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
         *reinterpret_cast<u32x2 *>(output + out_row + 32 * (2 * wave + j) + 8 * i4 + 4 * half) = w;
       }
   }
+  if constexpr (FromInput) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int idx = tid + kThreads * j;
+      const int pl = idx >> 8, tok = (idx >> 5) & 7, piece = idx & 31;
+      if (static_cast<std::size_t>(tok) < q_rows)
+        *reinterpret_cast<u32x4 *>(cache + pl * plane + cache_row(head_major, t0 + tok, kv_head, max_ctx) +
+                                   8 * piece) = app[j];
+    }
+  }
 }
 
 } // namespace
 
-void launch_prefill_mfma(const bf16_bits *q, const bf16_bits *gate, bf16_bits *out,
-                         const bf16_bits *cache, std::size_t tokens, std::size_t max_ctx,
-                         std::size_t past, bool head_major, hipStream_t stream) {
+void launch_prefill_mfma(const bf16_bits *q, const bf16_bits *key, const bf16_bits *value,
+                         const bf16_bits *gate, bf16_bits *out, bf16_bits *cache,
+                         std::size_t tokens, std::size_t max_ctx, std::size_t past,
+                         bool head_major, bool fused_append, hipStream_t stream) {
   // 8 workgroups (one per XCD) per pair of query tiles.
   const unsigned grid = static_cast<unsigned>(8 * ceil_div_unchecked(ceil_div_unchecked(tokens, kQTok), 2));
-  if (head_major)
-    prefill_mfma_kernel<true><<<grid, kThreads, 0, stream>>>(q, gate, out, cache, tokens, max_ctx, past);
-  else
-    prefill_mfma_kernel<false><<<grid, kThreads, 0, stream>>>(q, gate, out, cache, tokens, max_ctx, past);
+  if (fused_append) {
+    if (head_major)
+      prefill_mfma_kernel<true, true><<<grid, kThreads, 0, stream>>>(q, key, value, gate, out, cache,
+                                                                     tokens, max_ctx, past);
+    else
+      prefill_mfma_kernel<false, true><<<grid, kThreads, 0, stream>>>(q, key, value, gate, out, cache,
+                                                                      tokens, max_ctx, past);
+  } else if (head_major) {
+    prefill_mfma_kernel<true, false><<<grid, kThreads, 0, stream>>>(q, key, value, gate, out, cache,
+                                                                    tokens, max_ctx, past);
+  } else {
+    prefill_mfma_kernel<false, false><<<grid, kThreads, 0, stream>>>(q, key, value, gate, out, cache,
+                                                                     tokens, max_ctx, past);
+  }
 }
 
 } // namespace raftinfer::amd
