@@ -316,13 +316,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_single_mfma_kernel(
   }
 }
 
-template <int DS, int WAVES>
+template <int DS, int WAVES, int CT = 32>
 __global__ __launch_bounds__(WAVES * 64) void decode_split_mfma_kernel(
     DecodeMfmaArgs a, float *__restrict__ pmax, float *__restrict__ psum,
     float *__restrict__ pval, std::size_t host_position, const std::uint32_t *device_position,
     std::size_t capacity, std::size_t max_partitions, std::size_t partition_tokens,
     std::size_t threshold) {
-  __shared__ DecodeMfmaShared<DS, WAVES> sh;
+  __shared__ DecodeMfmaShared<DS, WAVES, CT> sh;
   constexpr int DIMS = kHeadDim / DS;
   const std::size_t position = read_position(device_position, host_position);
   if (position >= a.max_ctx) return;
@@ -337,7 +337,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_mfma_kernel(
   const std::size_t begin = partition * partition_tokens;
   if (begin >= ctx) return;
   const std::size_t end = ctx < begin + partition_tokens ? ctx : begin + partition_tokens;
-  decode_mfma_scan<DS, WAVES>(a, kv_head, dq, begin, end, position, sh);
+  decode_mfma_scan<DS, WAVES, CT>(a, kv_head, dq, begin, end, position, sh);
   __syncthreads();
   if (dq == 0 && position >= begin && position < end) append_rows(a, kv_head, position);
   for (int o = threadIdx.x; o < kGroup * DIMS; o += WAVES * 64) {

@@ -40,6 +40,9 @@ constexpr int kWaves = 4;            // key-split waves per workgroup
 constexpr int kThreads = kWaves * kWave;
 constexpr int kChunks = kHeadDim / 8; // 16-byte chunks per row
 constexpr float kLazyRescale = 8.0f; // log2 units
+#ifndef PV_BATCH
+#define PV_BATCH 8
+#endif
 
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4v lds_short4v;
@@ -278,12 +281,19 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
     // S^T = K Q^T: A row = key `col` of the tile (lane & 31), k-half `half`.
     // Chunk 2 kb + half of row `col` sits at (2 (kb & 3) + half) ^ (col & 7)
     // + 8 (kb >> 2): four lane bases plus constant offsets.
+    // Operands are read four MFMAs ahead (one batch per k_base group).
     floatx16 s = floatx16{};
 #pragma unroll
-    for (int kb = 0; kb < 16; ++kb)
-      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_b128(tile.k + k_base[kb & 3] + 64 * (kb >> 2)),
-                                                  lds_b128(sh.q + k_base[kb & 3] + 64 * (kb >> 2)),
-                                                  s, 0, 0, 0);
+    for (int k4 = 0; k4 < 4; ++k4) {
+      bf16x8 ka[4], qa[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        ka[j] = lds_b128(tile.k + k_base[j] + 64 * k4);
+        qa[j] = lds_b128(sh.q + k_base[j] + 64 * k4);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[j], qa[j], s, 0, 0, 0);
+    }
     wait_lgkm0(); // the K tile has been read
     if (more) issue(k_src, lds_k, k0 + kWaves * kKTile);
 
@@ -340,16 +350,25 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
     // Row 16 kb + trow (+ 8) and dim 32 nb + dsub: the swizzle key is trow & 7
     // for every row read, so two lane bases (nb & 1) plus constant offsets
     // (rows 16 kb (+8), chunk 8 (nb >> 1)) cover all 32 reads.
+    // The operands of PV_BATCH MFMAs are read before any of them is issued, so
+    // the LDS latency is paid once per batch rather than once per MFMA.
     {
+      constexpr int kBatch = PV_BATCH;
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb) {
+      for (int b0 = 0; b0 < 16; b0 += kBatch) {
+        bf16x8 av[kBatch];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+        for (int j = 0; j < kBatch; ++j) {
+          const int nb = (b0 + j) >> 1, kb = (b0 + j) & 1;
           const bf16_bits *v0 = tile.v + v_base[nb & 1] + 64 * (nb >> 1) + kHeadDim * 16 * kb;
           const u32x2 lo = lds_tr16(v0);
           const u32x2 hi = lds_tr16(v0 + kHeadDim * 8);
-          const bf16x8 a = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-          mfma_acc_agpr(o[nb], a, pw[kb]);
+          av[j] = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          const int nb = (b0 + j) >> 1, kb = (b0 + j) & 1;
+          mfma_acc_agpr(o[nb], av[j], pw[kb]);
         }
       }
       mfma_drain(); // the accumulators may be read by VALU code below

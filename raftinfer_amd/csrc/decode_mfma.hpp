@@ -31,22 +31,22 @@ struct DecodeMfmaArgs {
   bool head_major;
 };
 
-template <int DS, int WAVES> struct DecodeMfmaShared {
+template <int DS, int WAVES, int CT = 32> struct DecodeMfmaShared {
   static constexpr int DIMS = kHeadDim / DS;
-  float p[WAVES][32][4];
+  float p[WAVES][CT][4];
   float m[WAVES][4];
   float l[WAVES][4];
   float acc[WAVES][4][DIMS];
 };
 
-// PV lane mapping for a DIMS-wide slice: a lane owns VEC consecutive dims
-// (one 2*VEC-byte load per token) and one of TL token phases.
-template <int DIMS> struct PvMap {
+// PV lane mapping for a DIMS-wide slice and CT-token chunks: a lane owns VEC
+// consecutive dims (one 2*VEC-byte load per token) and one of TL token phases.
+template <int DIMS, int CT = 32> struct PvMap {
   static constexpr int VEC = DIMS / 8 > 8 ? 8 : DIMS / 8;
   static constexpr int DL = DIMS / VEC;
   static constexpr int TL = 64 / DL;
-  static constexpr int TPL = 32 / TL;
-  static_assert(DL * VEC == DIMS && DL * TL == 64 && TPL * TL == 32 && DL >= 8, "bad PV map");
+  static constexpr int TPL = CT / TL;
+  static_assert(DL * VEC == DIMS && DL * TL == 64 && TPL * TL == CT && DL >= 8, "bad PV map");
 };
 
 template <int VEC> struct VRow {
@@ -87,12 +87,13 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // over half of the line and the score is C[2t][h] + C[2t+1][4+h], two values
 // 4 lanes apart in a row (one DPP add).  After it, lane l with l%16 < 4 holds
 // head l%16's scores of tokens 2*(l/16) and 2*(l/16)+1 of the group.
-template <int DS, int WAVES>
+template <int DS, int WAVES, int CT = 32>
 __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::size_t kv_head,
                                                  int dq, std::size_t begin, std::size_t end,
-                                                 std::size_t pos, DecodeMfmaShared<DS, WAVES> &sh) {
+                                                 std::size_t pos, DecodeMfmaShared<DS, WAVES, CT> &sh) {
   constexpr int DIMS = kHeadDim / DS;
-  using Map = PvMap<DIMS>;
+  constexpr int G = CT / 8; // 8-token groups per chunk
+  using Map = PvMap<DIMS, CT>;
   constexpr int VEC = Map::VEC, DL = Map::DL, TL = Map::TL, TPL = Map::TPL;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -127,13 +128,13 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[h][e] = 0.f;
 
-  for (std::size_t c0 = begin + static_cast<std::size_t>(wave) * 32; c0 < end;
-       c0 += static_cast<std::size_t>(WAVES) * 32) {
+  for (std::size_t c0 = begin + static_cast<std::size_t>(wave) * CT; c0 < end;
+       c0 += static_cast<std::size_t>(WAVES) * CT) {
     // Issue every load of the chunk first: K for the scores, V for the slice.
     // Tokens past `end` read row end-1 (in bounds); they are masked below.
-    u32x4 kr[4][4];
+    u32x4 kr[G][4];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
+    for (int g = 0; g < G; ++g) {
       std::size_t tok = c0 + 8 * g + rt;
       tok = tok < end ? tok : end - 1;
       const bf16_bits *row = tok == pos ? a.key_new + kv_head * kHeadDim
@@ -155,10 +156,10 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
     // otherwise sinks V loads below the K waits, adding a second round trip.
     __builtin_amdgcn_sched_barrier(0);
     // Scores of tokens c0 + 8g + 2kq + {0, 1} for head n (head lanes).
-    float sg[4][2];
+    float sg[G][2];
     float mx = -INFINITY;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
+    for (int g = 0; g < G; ++g) {
       floatx4 c = floatx4{};
 #pragma unroll
       for (int line = 0; line < 4; ++line)
@@ -178,7 +179,7 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
     const float sc = fast_exp2(m_run - m_new); // m_run = -inf -> 0
     float psum = 0.f;
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
+    for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const float p = fast_exp2(sg[g][t] - m_new);
@@ -252,8 +253,8 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
   }
 }
 
-template <int DS, int WAVES>
-__device__ __forceinline__ void decode_mfma_combine(const DecodeMfmaShared<DS, WAVES> &sh, int h,
+template <int DS, int WAVES, int CT>
+__device__ __forceinline__ void decode_mfma_combine(const DecodeMfmaShared<DS, WAVES, CT> &sh, int h,
                                                     int d, float &m_out, float &l_out,
                                                     float &a_out) {
   float mm = -INFINITY;
