@@ -200,29 +200,31 @@ __global__ __launch_bounds__(WAVES * 64) void decode_partition_kernel(
 // partitions are independent.  A device position needing more partitions than
 // the plan's capacity writes NaN and counts a capacity error instead of
 // trapping.
-constexpr int kMergeChunk = 32;
+constexpr int kMergeChunk = 32;      // partitions per round trip (long contexts)
+constexpr int kMergeChunkShort = 16; // when the plan's capacity is at most 16 partitions
+constexpr int kMergeDims = 64;       // dims per merge workgroup (one thread each)
 
-// Merges the partials of one head online over chunks of kMergeChunk
-// partitions; thread d owns output dim d.  Lane u of every wave reads the
+// Merges the partials of one head online over chunks of CH partitions;
+// the calling thread owns output dim d.  Lane u of every wave reads the
 // max and sum of partition base + u, the chunk max and the sum of weighted
 // sums are lane reductions, and lane u's weight reaches the other lanes by
 // v_readlane.  Every load of a chunk is issued before any is used, so a
 // chunk costs one memory round trip.
-__device__ __forceinline__ void merge_head(const float *__restrict__ pmax,
+template <int CH = kMergeChunk>
+__device__ __forceinline__ void merge_head(int d, const float *__restrict__ pmax,
                                            const float *__restrict__ psum,
                                            const float *__restrict__ pval, std::size_t first,
                                            std::size_t active, float &l_out, float &a_out) {
-  const int d = threadIdx.x;
-  const int lane = d & 63;
+  const int lane = threadIdx.x & 63;
   float m = -INFINITY, l = 0.f, a = 0.f;
-  for (std::size_t base = 0; base < active; base += kMergeChunk) {
-    const std::size_t n = active - base < kMergeChunk ? active - base : kMergeChunk;
+  for (std::size_t base = 0; base < active; base += CH) {
+    const std::size_t n = active - base < CH ? active - base : CH;
     const std::size_t pl = first + base + (static_cast<std::size_t>(lane) < n ? lane : n - 1);
     const float mraw = pmax[pl];
     const float sraw = psum[pl];
-    float vx[kMergeChunk];
+    float vx[CH];
 #pragma unroll
-    for (int u = 0; u < kMergeChunk; ++u) {
+    for (int u = 0; u < CH; ++u) {
       const std::size_t p = first + base + (static_cast<std::size_t>(u) < n ? u : n - 1);
       vx[u] = pval[p * kHeadDim + d];
     }
@@ -234,7 +236,7 @@ __device__ __forceinline__ void merge_head(const float *__restrict__ pmax,
     l = fmaf(l, r, sum_xor32(sum_xor16(row16_sum(sraw * w))));
     a *= r;
 #pragma unroll
-    for (int u = 0; u < kMergeChunk; ++u) {
+    for (int u = 0; u < CH; ++u) {
       if (static_cast<std::size_t>(u) < n)
         a = fmaf(vx[u], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), u)), a);
     }
@@ -244,8 +246,8 @@ __device__ __forceinline__ void merge_head(const float *__restrict__ pmax,
   a_out = a;
 }
 
-template <typename ActT>
-__global__ __launch_bounds__(256) void decode_merge_kernel(
+template <typename ActT, int CH = kMergeChunk>
+__global__ __launch_bounds__(kMergeDims) void decode_merge_kernel(
     const ActT *__restrict__ gate, ActT *__restrict__ output, const float *__restrict__ pmax,
     const float *__restrict__ psum, const float *__restrict__ pval, std::size_t max_ctx,
     std::size_t host_position, std::size_t partition_tokens, std::size_t max_partitions,
@@ -255,17 +257,18 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(
   const std::size_t ctx = position + 1;
   if (ctx < threshold) return;
   const std::size_t active = ctx / partition_tokens + (ctx % partition_tokens ? 1 : 0);
-  const std::size_t head = blockIdx.x;
-  const int d = threadIdx.x;
+  // Workgroup = (head, block of kMergeDims dims); thread = dim.
+  const std::size_t head = blockIdx.x / (kHeadDim / kMergeDims);
+  const int d = static_cast<int>(blockIdx.x % (kHeadDim / kMergeDims)) * kMergeDims + threadIdx.x;
   const std::size_t out_idx = head * kHeadDim + d;
   if (active > capacity) {
-    if (head == 0 && d == 0) atomicAdd(&g_capacity_errors, 1u);
+    if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&g_capacity_errors, 1u);
     Elem<ActT>::store(output, out_idx, __builtin_nanf(""));
     return;
   }
   const float gv = Elem<ActT>::load(gate, out_idx);
   float l, a;
-  merge_head(pmax, psum, pval, head * max_partitions, active, l, a);
+  merge_head<CH>(d, pmax, psum, pval, head * max_partitions, active, l, a);
   Elem<ActT>::store(output, out_idx, (a / l) * sigmoid_gate(gv));
 }
 
@@ -355,6 +358,23 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_mfma_kernel(
 
 // ------------------------------------------------------------ launchers
 
+// The merge reads every active partition in one round trip per chunk; a plan
+// whose capacity fits one 16-partition chunk uses the shorter chunk.
+template <typename ActT>
+void launch_merge(const ActT *g, ActT *out, const float *pmax, const float *psum, const float *pval,
+                  Qwen35AttentionShape shape, Qwen35OnlineDecodePlan plan, std::size_t max_partitions,
+                  const std::uint32_t *device_position, hipStream_t stream) {
+  constexpr unsigned grid = kQueryHeads * (kHeadDim / kMergeDims);
+  if (plan.active_partition_capacity <= static_cast<std::size_t>(kMergeChunkShort))
+    decode_merge_kernel<ActT, kMergeChunkShort><<<grid, kMergeDims, 0, stream>>>(
+        g, out, pmax, psum, pval, shape.max_context_tokens, shape.past_tokens, plan.partition_tokens,
+        max_partitions, plan.active_partition_capacity, plan.split_k_threshold_tokens, device_position);
+  else
+    decode_merge_kernel<ActT, kMergeChunk><<<grid, kMergeDims, 0, stream>>>(
+        g, out, pmax, psum, pval, shape.max_context_tokens, shape.past_tokens, plan.partition_tokens,
+        max_partitions, plan.active_partition_capacity, plan.split_k_threshold_tokens, device_position);
+}
+
 constexpr int kSingleHeads = 1, kSingleWaves = 16, kSingleUnroll = 2;
 constexpr int kPartHeads = 4, kPartWaves = 8, kPartUnroll = 2;
 
@@ -415,10 +435,7 @@ void launch_decode(const void *query, const void *key, const void *value, const 
                           ? "qwen35_online_attention_decode_split_k_256_partition"
                           : "qwen35_online_attention_decode_split_k_512_partition");
     if (partition_only) return;
-    decode_merge_kernel<ActT><<<kQueryHeads, 256, 0, stream>>>(
-        g, out, pmax, psum, pval, shape.max_context_tokens, shape.past_tokens,
-        plan.partition_tokens, max_partitions, plan.active_partition_capacity,
-        plan.split_k_threshold_tokens, device_position);
+    launch_merge<ActT>(g, out, pmax, psum, pval, shape, plan, max_partitions, device_position, stream);
     check_launch<Err>("qwen35_online_attention_decode_split_k_merge");
     return;
   }
@@ -465,10 +482,7 @@ void launch_decode(const void *query, const void *key, const void *value, const 
   check_launch<Err>(plan.partition_tokens == 256
                         ? "qwen35_online_attention_decode_split_k_256_partition"
                         : "qwen35_online_attention_decode_split_k_512_partition");
-  decode_merge_kernel<ActT><<<kQueryHeads, 256, 0, stream>>>(
-      g, out, pmax, psum, pval, shape.max_context_tokens, shape.past_tokens,
-      plan.partition_tokens, max_partitions, plan.active_partition_capacity,
-      plan.split_k_threshold_tokens, device_position);
+  launch_merge<ActT>(g, out, pmax, psum, pval, shape, plan, max_partitions, device_position, stream);
   check_launch<Err>("qwen35_online_attention_decode_split_k_merge");
 }
 
@@ -741,7 +755,8 @@ __global__ __launch_bounds__(256) void batched_merge_kernel(
   const std::size_t out_idx = (seq * kQueryHeads + head) * kHeadDim + threadIdx.x;
   const float gv = Elem<ActT>::load(gate, out_idx);
   float l, a;
-  merge_head(pmax, psum, pval, (seq * kQueryHeads + head) * max_partitions, active, l, a);
+  merge_head(static_cast<int>(threadIdx.x), pmax, psum, pval, (seq * kQueryHeads + head) * max_partitions,
+             active, l, a);
   Elem<ActT>::store(output, out_idx, (a / l) * sigmoid_gate(gv));
 }
 
