@@ -16,7 +16,9 @@ the CPU oracle's decode on one host core over a bounded sample.
 ``--counters`` launches the ctx-4096 partition kernel eagerly (no graph) 20
 times on 20 distinct caches, then copies a 64 MiB buffer 20 times with a
 plain device-to-device copy kernel of known size, so that FETCH_SIZE and
-WRITE_SIZE per dispatch can be scaled by what the counters read for the copy.
+WRITE_SIZE per dispatch can be scaled by what the counters read for the copy;
+then 20 PP512 prefill kernels, 10 delta prefills (T=512) and 20 delta decode
+steps, for their traffic and MFMA counters.
 """
 from __future__ import annotations
 
@@ -148,7 +150,42 @@ def main():
         for _ in range(20):
             dst.copy_(src)
         torch.cuda.synchronize()
-        log("counters run: 20 partition launches (ctx 4096) + 20 copies of 64 MiB")
+        del src, dst
+        # PP512 prefill (kernel with the fused append) and the cfg5 delta
+        # prefill / decode step, launched eagerly for per-dispatch counters.
+        from raftinfer_amd import _lib
+        import ctypes
+        lib = _lib.load()
+        T = 512
+        shape = ops.Qwen35AttentionShape(T, HQ, HKV, D, T, 0)
+        qp, gp = rand_bf16(T * HQ * D), rand_bf16(T * HQ * D)
+        kp, vp = rand_bf16(T * HKV * D), rand_bf16(T * HKV * D)
+        cache = torch.zeros(2 * T * HKV * D, device="cuda", dtype=torch.bfloat16)
+        outp = torch.empty(T * HQ * D, device="cuda", dtype=torch.bfloat16)
+        for _ in range(20):
+            _lib.check(lib.raftinfer_amd_online_attention_prefill_kernel_only(
+                *[ctypes.c_void_p(t.data_ptr()) for t in (qp, kp, vp, gp, outp, cache)],
+                cache.numel() * 2, shape.c(), ops.DTYPE_BF16, ops.CACHE_BF16, ops.HEAD_MAJOR,
+                ctypes.c_void_p(stream.cuda_stream)))
+        q5 = torch.nn.functional.normalize(torch.randn(T, 16, 128, device="cuda"), dim=-1).to(torch.bfloat16)
+        k5 = torch.nn.functional.normalize(torch.randn(T, 16, 128, device="cuda"), dim=-1).to(torch.bfloat16)
+        v5 = rand_bf16(T, 32, 128)
+        beta = torch.sigmoid(torch.randn(T, 32, device="cuda"))
+        lg = -torch.nn.functional.softplus(torch.randn(T, 32, device="cuda"))
+        st = torch.zeros(32, 128, 128, device="cuda")
+        o5 = torch.empty(T, 32, 128, device="cuda", dtype=torch.bfloat16)
+        ws5 = torch.empty(ops.qwen35_gated_delta_core_workspace_bytes(T, 16, 32, 128, 128),
+                          device="cuda", dtype=torch.uint8)
+        for _ in range(10):
+            ops.qwen35_gated_delta_core(q5, k5, v5, beta, lg, 128 ** -0.5, st, o5, ws5, True,
+                                        stream=stream)
+        for i in range(20):
+            ops.qwen35_gated_delta_core(q5[i:i + 1], k5[i:i + 1], v5[i:i + 1], beta[i:i + 1],
+                                        lg[i:i + 1], 128 ** -0.5, st, o5[:1], None, False,
+                                        stream=stream)
+        torch.cuda.synchronize()
+        log("counters run: 20 partition launches (ctx 4096), 20 copies of 64 MiB, 20 PP512 "
+            "prefill kernels, 10 delta prefills (T=512), 20 delta decode steps")
         return
 
     us4096, kus4096 = split_decode(4096, 40)
