@@ -455,6 +455,96 @@ __global__ __launch_bounds__(kRecWaves * 64) void recurrent_kernel(
   }
 }
 
+// Model-shape recurrence (dk = dv = 128), block (value head, 32-column
+// block), 256 threads: thread (row group rg = tid / 8, column quad cq =
+// tid % 8) holds S[4 rg .. 4 rg + 3][c0 + 4 cq .. + 3] as four float4 rows, so
+// every state load or store instruction of a wave covers 8 whole 128-byte
+// rows.  The sums over the 128 rows run as a butterfly over the 8 row groups
+// of a wave (lanes ^ 8, ^ 16, ^ 32) and an LDS sum over the 4 waves; every
+// thread then holds kv (and o) of its 4 columns.  Same update order as the
+// generic kernel: S *= decay; kv = S^T k; delta = beta (v - kv); S += k delta;
+// o = S^T q.
+constexpr int kRec128Cols = 32;
+template <typename InT, typename OutT>
+__global__ __launch_bounds__(256) void recurrent_128_kernel(
+    Src<InT> qs, Src<InT> ks, Src<InT> vs, const float *__restrict__ beta,
+    const float *__restrict__ gdecay, float *__restrict__ state, OutT *__restrict__ out,
+    std::size_t tokens, std::size_t hk, std::size_t hv) {
+  constexpr int kDim = 128;
+  __shared__ float4 red[2][4][kRec128Cols / 4]; // [kv / o][wave][column quad]
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const int cq = tid & 7, rg = tid >> 3;
+  const std::size_t h = blockIdx.x;
+  const std::size_t kh = h % hk;
+  const int c0 = blockIdx.y * kRec128Cols + 4 * cq;
+  float *sh = state + h * kDim * kDim;
+  float4 s[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s[i] = *reinterpret_cast<const float4 *>(sh + (4 * rg + i) * kDim + c0);
+  auto row_sum = [&](float4 x, int which) {
+    // lanes ^ 8 (DPP row_ror:8), ^ 16, ^ 32 hold the other row groups of
+    // this wave for the same column quad.
+    x.x = sum_xor32(sum_xor16(sum_xor8(x.x)));
+    x.y = sum_xor32(sum_xor16(sum_xor8(x.y)));
+    x.z = sum_xor32(sum_xor16(sum_xor8(x.z)));
+    x.w = sum_xor32(sum_xor16(sum_xor8(x.w)));
+    if ((tid & 63) < 8) red[which][wave][cq] = x;
+    __syncthreads();
+    float4 t = red[which][0][cq];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      const float4 u = red[which][w][cq];
+      t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+    }
+    return t;
+  };
+  for (std::size_t t = 0; t < tokens; ++t) {
+    const float b = beta[t * hv + h];
+    const float decay = __expf(gdecay[t * hv + h]);
+    float kr[4], qr[4], vv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kr[i] = ks.at(t, kh, 4 * rg + i);
+      qr[i] = qs.at(t, kh, 4 * rg + i);
+      vv[i] = vs.at(t, h, c0 + i);
+    }
+    float4 part = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s[i].x *= decay; s[i].y *= decay; s[i].z *= decay; s[i].w *= decay;
+      part.x = fmaf(s[i].x, kr[i], part.x);
+      part.y = fmaf(s[i].y, kr[i], part.y);
+      part.z = fmaf(s[i].z, kr[i], part.z);
+      part.w = fmaf(s[i].w, kr[i], part.w);
+    }
+    const float4 kv = row_sum(part, 0);
+    const float4 d = make_float4((vv[0] - kv.x) * b, (vv[1] - kv.y) * b, (vv[2] - kv.z) * b,
+                                 (vv[3] - kv.w) * b);
+    float4 po = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s[i].x = fmaf(kr[i], d.x, s[i].x);
+      s[i].y = fmaf(kr[i], d.y, s[i].y);
+      s[i].z = fmaf(kr[i], d.z, s[i].z);
+      s[i].w = fmaf(kr[i], d.w, s[i].w);
+      po.x = fmaf(s[i].x, qr[i], po.x);
+      po.y = fmaf(s[i].y, qr[i], po.y);
+      po.z = fmaf(s[i].z, qr[i], po.z);
+      po.w = fmaf(s[i].w, qr[i], po.w);
+    }
+    const float4 o = row_sum(po, 1);
+    if (rg == 0) {
+      const std::size_t base = (t * hv + h) * kDim + c0;
+      Elem<OutT>::store(out, base, o.x);
+      Elem<OutT>::store(out, base + 1, o.y);
+      Elem<OutT>::store(out, base + 2, o.z);
+      Elem<OutT>::store(out, base + 3, o.w);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) *reinterpret_cast<float4 *>(sh + (4 * rg + i) * kDim + c0) = s[i];
+}
+
 // ------------------------------------------------- stage 2b: chunked
 // fp32 MFMA 16x16x4: lane l supplies A[l%16][l/16] and B[l/16][l%16] and
 // holds D[(l/16)*4 + r][l%16], r = 0..3.
@@ -1240,6 +1330,12 @@ void launch_recurrence(Src<InT> q, Src<InT> k, Src<InT> v, const float *beta, co
                                                               exact ? q.scale : 1.0f,
                                                               exact ? k.scale : 1.0f);
     check_launch<Err>("qwen35_gated_delta chunk scan");
+    return;
+  }
+  if (dk == 128 && dv == 128 && (reinterpret_cast<std::uintptr_t>(state) & 15u) == 0) {
+    const dim3 g128{static_cast<unsigned>(hv), 128 / kRec128Cols, 1};
+    recurrent_128_kernel<InT, OutT><<<g128, 256, 0, stream>>>(q, k, v, beta, g, state, out, tokens, hk, hv);
+    check_launch<Err>("qwen35_gated_delta register recurrent update");
     return;
   }
   const dim3 grid{static_cast<unsigned>(hv), static_cast<unsigned>(ceil_div_unchecked(dv, 64)), 1};
