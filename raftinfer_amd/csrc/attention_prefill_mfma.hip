@@ -16,8 +16,9 @@
 //               tile.  Rows are stored as 32 16-byte chunks with chunk c at
 //               c ^ swz(row), so both operand reads below are free of bank
 //               conflicts;
-//   S^T = K Q^T 16 x v_mfma_f32_32x32x16_bf16, K rows read from LDS with
-//               ds_read_b128, Q^T held in VGPRs for the whole kernel;
+//   S^T = K Q^T 16 x v_mfma_f32_32x32x16_bf16, K and Q rows read from LDS
+//               with ds_read_b128 four MFMAs ahead (the Q tile is staged once
+//               per workgroup, in the K tile's chunk order);
 //   softmax     online in the exp2 domain; lane l owns column l % 32 and 16
 //               of the tile's keys; the reference max moves only when a
 //               column max grows by more than 2^8 (lazy rescaling);
@@ -25,9 +26,12 @@
 //               S^T accumulator's key order, and the V^T operand is read in
 //               that order straight from the row-major V tile with
 //               ds_read_b64_tr_b16 (lane i of a 16-lane group receives 4 keys
-//               of one dim).
+//               of one dim), eight MFMAs' operands at a time.  The O^T
+//               accumulators stay in AGPRs (inline-asm MFMA).
 // The waves' partial (max, sum, O) are merged through LDS at the end; wave w
-// finishes dims [64w, 64w+64) and applies the sigmoid gate.
+// finishes dims [64w, 64w+64) and applies the sigmoid gate, whose loads were
+// issued at the start.  With past == 0 the keys come from the key/value
+// inputs and each workgroup also writes its 8 tokens' cache rows (the append).
 #include "decode_scan.hpp"
 #include "prefill_mfma.hpp"
 
@@ -38,11 +42,8 @@ constexpr int kQTok = 8;             // query tokens per workgroup
 constexpr int kKTile = 32;           // keys per tile
 constexpr int kWaves = 4;            // key-split waves per workgroup
 constexpr int kThreads = kWaves * kWave;
-constexpr int kChunks = kHeadDim / 8; // 16-byte chunks per row
 constexpr float kLazyRescale = 8.0f; // log2 units
-#ifndef PV_BATCH
-#define PV_BATCH 8
-#endif
+constexpr int kPvBatch = 8;          // PV MFMAs whose operands are read together
 
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4v lds_short4v;
@@ -350,10 +351,10 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
     // Row 16 kb + trow (+ 8) and dim 32 nb + dsub: the swizzle key is trow & 7
     // for every row read, so two lane bases (nb & 1) plus constant offsets
     // (rows 16 kb (+8), chunk 8 (nb >> 1)) cover all 32 reads.
-    // The operands of PV_BATCH MFMAs are read before any of them is issued, so
+    // The operands of kPvBatch MFMAs are read before any of them is issued, so
     // the LDS latency is paid once per batch rather than once per MFMA.
     {
-      constexpr int kBatch = PV_BATCH;
+      constexpr int kBatch = kPvBatch;
 #pragma unroll
       for (int b0 = 0; b0 < 16; b0 += kBatch) {
         bf16x8 av[kBatch];
