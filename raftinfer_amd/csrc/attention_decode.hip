@@ -202,6 +202,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_partition_kernel(
 // trapping.
 constexpr int kMergeChunk = 32;      // partitions per round trip (long contexts)
 constexpr int kMergeChunkShort = 16; // when the plan's capacity is at most 16 partitions
+constexpr int kMergeChunkLong = 64;  // when it is at most 64 (one round trip up to ctx 16384 at P=256)
 constexpr int kMergeDims = 64;       // dims per merge workgroup (one thread each)
 
 // Merges the partials of one head online over chunks of CH partitions;
@@ -358,8 +359,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_mfma_kernel(
 
 // ------------------------------------------------------------ launchers
 
-// The merge reads every active partition in one round trip per chunk; a plan
-// whose capacity fits one 16-partition chunk uses the shorter chunk.
+// The merge reads every active partition in one round trip per chunk; the
+// chunk is the smallest of 16, 64 or 32 (the general case) that holds the
+// plan's capacity in one round trip.
 template <typename ActT>
 void launch_merge(const ActT *g, ActT *out, const float *pmax, const float *psum, const float *pval,
                   Qwen35AttentionShape shape, Qwen35OnlineDecodePlan plan, std::size_t max_partitions,
@@ -367,6 +369,10 @@ void launch_merge(const ActT *g, ActT *out, const float *pmax, const float *psum
   constexpr unsigned grid = kQueryHeads * (kHeadDim / kMergeDims);
   if (plan.active_partition_capacity <= static_cast<std::size_t>(kMergeChunkShort))
     decode_merge_kernel<ActT, kMergeChunkShort><<<grid, kMergeDims, 0, stream>>>(
+        g, out, pmax, psum, pval, shape.max_context_tokens, shape.past_tokens, plan.partition_tokens,
+        max_partitions, plan.active_partition_capacity, plan.split_k_threshold_tokens, device_position);
+  else if (plan.active_partition_capacity <= static_cast<std::size_t>(kMergeChunkLong))
+    decode_merge_kernel<ActT, kMergeChunkLong><<<grid, kMergeDims, 0, stream>>>(
         g, out, pmax, psum, pval, shape.max_context_tokens, shape.past_tokens, plan.partition_tokens,
         max_partitions, plan.active_partition_capacity, plan.split_k_threshold_tokens, device_position);
   else
