@@ -80,30 +80,7 @@ __device__ __forceinline__ u32x2 lds_tr16(const bf16_bits *p) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v *)(p)));
 }
 
-// LDS byte address of a __shared__ object.
-template <typename T> __device__ __forceinline__ unsigned lds_address(T *p) {
-  return static_cast<unsigned>(reinterpret_cast<std::uintptr_t>(
-      (__attribute__((address_space(3))) char *)(p)));
-}
 
-// 16 bytes from base + voff (per lane) into LDS at lds + 16 * lane
-// (global_load_lds_dwordx4).  Written as asm, with the waits below issued by
-// hand: the compiler cannot tell which LDS tile such a load writes and would
-// otherwise wait for every outstanding one before each LDS read.  The kernel
-// uses no other instruction that reads M0.
-__device__ __forceinline__ void load_lds_b128(const void *base, std::uint32_t voff, unsigned lds) {
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :
-               : "s"(lds), "v"(voff), "s"(base)
-               : "memory", "m0");
-#pragma clang diagnostic pop
-}
-template <int N> __device__ __forceinline__ void wait_vm() {
-  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
-}
-__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory"); }
 
 __host__ __device__ constexpr std::size_t ceil_div_u(std::size_t n, std::size_t d) {
   return (n + d - 1) / d;

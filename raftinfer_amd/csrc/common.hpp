@@ -190,6 +190,32 @@ __device__ __forceinline__ void wave_lds_order() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// ------------------------------------------------ LDS-direct loads
+// LDS byte address of a __shared__ object.
+template <typename T> __device__ __forceinline__ unsigned lds_address(T *p) {
+  return static_cast<unsigned>(reinterpret_cast<std::uintptr_t>(
+      (__attribute__((address_space(3))) char *)(p)));
+}
+
+// 16 bytes from base + voff (per lane) into LDS at lds + 16 * lane
+// (global_load_lds_dwordx4).  Written as asm, with the waits below issued by
+// hand: the compiler cannot tell which LDS region such a load writes and
+// would otherwise wait for every outstanding one before each LDS read.  The
+// kernels that use it issue no other instruction that reads M0.
+__device__ __forceinline__ void load_lds_b128(const void *base, std::uint32_t voff, unsigned lds) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds), "v"(voff), "s"(base)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
+template <int N> __device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory"); }
+
 // ------------------------------------------------------ host utilities
 template <typename Error> inline void require(bool condition, const char *message) {
   if (!condition) throw Error(message);

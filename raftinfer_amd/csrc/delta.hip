@@ -1077,16 +1077,28 @@ __global__ __launch_bounds__(256) void chunk_prep_bf16_kernel(Src<bf16_bits> qs,
 constexpr int kLdK = kChunkDim + 8; // bf16 row stride for 128-long k
 constexpr int kLdJ = kChunk + 8;    // bf16 row stride for 64-long k
 
+// Chunk operands W, Q, M (rows i) and K^T (rows d) are loaded from the chunk
+// record straight into LDS (global_load_lds_dwordx4) in unpadded rows whose
+// 16-byte chunks are XOR-swizzled by row, so the MFMA operand reads (16
+// rows x one chunk per lane group) hit distinct banks: 128-wide rows (16
+// chunks) use chunk ^ (row & 15), 64-wide rows (8 chunks, two rows per bank
+// window) chunk ^ ((row >> 1) & 7).  Every wave reads only its own rows of
+// these four blocks (W, Q, M rows 16w.., K^T rows 32w..), so each wave loads
+// its own rows and waits for them alone.
 struct Scan3Shared {
-  bf16_bits w[2][kChunk][kLdK];      // W (hi, lo), [i][d]
-  bf16_bits q[2][kChunk][kLdK];      // Q (hi, lo), [i][d]
-  bf16_bits kt[2][kChunkDim][kLdJ];  // K^T (hi, lo), [d][j]
-  bf16_bits m[2][kChunk][kLdJ];      // M (hi, lo), [i][j]
-  bf16_bits st[2][kColBlock][kLdK];  // S^T (hi, lo), [c][d]
-  bf16_bits dt[2][kColBlock][kLdJ];  // D^T (hi, lo), [c][i]
-  bf16_bits ft[2][kColBlock][kLdJ];  // (e^{G_last-G} D)^T (hi, lo), [c][j]
-  float g[kChunk];                   // cumulative log decay G of the chunk
+  bf16_bits w[2][kChunk][kChunkDim];   // W (hi, lo), [i][d]
+  bf16_bits q[2][kChunk][kChunkDim];   // Q (hi, lo), [i][d]
+  bf16_bits kt[2][kChunkDim][kChunk];  // K^T (hi, lo), [d][j]
+  bf16_bits m[2][kChunk][kChunk];      // M (hi, lo), [i][j]
+  bf16_bits st[2][kColBlock][kLdK];    // S^T (hi, lo), [c][d]
+  bf16_bits dt[2][kColBlock][kLdJ];    // D^T (hi, lo), [c][i]
+  bf16_bits ft[2][kColBlock][kLdJ];    // (e^{G_last-G} D)^T (hi, lo), [c][j]
+  float u[kChunk][kColBlock];          // U[i][c0 ..], this block's columns
+  float g[2][kChunk];                  // cumulative log decay G, by chunk parity
 };
+// Element offset of logical 16-byte chunk c in row r of a swizzled block.
+__device__ __forceinline__ int swz128(int r, int c) { return r * kChunkDim + ((c ^ (r & 15)) << 3); }
+__device__ __forceinline__ int swz64(int r, int c) { return r * kChunk + ((c ^ ((r >> 1) & 7)) << 3); }
 
 __device__ __forceinline__ bf16x8 lds8(const bf16_bits *p) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(p));
@@ -1095,69 +1107,27 @@ __device__ __forceinline__ floatx4 mfma_bf16(const bf16_bits *a, const bf16_bits
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(lds8(a), lds8(b), c, 0, 0, 0);
 }
 
-// One chunk record's operands, held in registers so the next chunk's loads
-// are in flight while the current chunk is computed.  Item n of a [2][R][C]
-// bf16 block is its 16-byte piece n (pieces are row-major, C/8 per row).
-template <bool kExact> struct ScanRegs {
-  // bf16 q / k inputs (kExact) have no low part in the record.
-  static constexpr int kQK = kExact ? 4 : 8;
-  u32x4 w[8], q[kQK], kt[kQK], m[4];
-  floatx4 u; // U[16 wave + 4 (lane / 16) + r][c0 + lane % 16]
-  float g;
-  // The loads are issued in three parts, one ahead of each MFMA phase of the
-  // current chunk, so the load path works while the matrix cores do.
-  __device__ __forceinline__ void load_part(int part, const unsigned char *record, int c0) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (part == 0) {
-      const u32x4 *pw = reinterpret_cast<const u32x4 *>(record + rec::kW);
+// LDS-direct load of rows row0 .. row0+ROWS-1 of halves 0 .. HALVES-1 of a
+// bf16 [2][R][C] record block at byte offset `off` into its swizzled LDS copy
+// `dst` (same shape).  One instruction moves 1 KiB = 1024 / (2 C) rows; lane
+// i fills physical chunk i % (C / 8) of its row with the logical chunk that
+// the swizzle puts there.  row0 is wave-uniform.
+template <int R, int C, int ROWS, int HALVES>
+__device__ __forceinline__ void load_rows_lds(const unsigned char *record, std::uint32_t off,
+                                              bf16_bits (*dst)[R][C], int row0) {
+  constexpr int kCpr = C / 8, kRpi = 64 / kCpr;
+  const int lane = threadIdx.x & 63;
+  const int rr = lane / kCpr, p = lane % kCpr;
 #pragma unroll
-      for (int n = 0; n < 8; ++n) w[n] = pw[tid + 256 * n];
-      const float *pu = reinterpret_cast<const float *>(record + rec::kU) + c0 + (lane & 15);
+  for (int hl = 0; hl < HALVES; ++hl)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) u[r] = pu[(wave * 16 + (lane >> 4) * 4 + r) * kChunkDim];
-      g = reinterpret_cast<const float *>(record + rec::kG)[tid & (kChunk - 1)];
-    } else if (part == 1) {
-      const u32x4 *pq = reinterpret_cast<const u32x4 *>(record + rec::kQ);
-      const u32x4 *pm = reinterpret_cast<const u32x4 *>(record + rec::kM);
-#pragma unroll
-      for (int n = 0; n < kQK; ++n) q[n] = pq[tid + 256 * n];
-#pragma unroll
-      for (int n = 0; n < 4; ++n) m[n] = pm[tid + 256 * n];
-    } else {
-      const u32x4 *pk = reinterpret_cast<const u32x4 *>(record + rec::kKt);
-#pragma unroll
-      for (int n = 0; n < kQK; ++n) kt[n] = pk[tid + 256 * n];
+    for (int j = 0; j < ROWS / kRpi; ++j) {
+      const int row = row0 + j * kRpi + rr;
+      const int logical = C == kChunkDim ? p ^ (row & 15) : p ^ ((row >> 1) & 7);
+      load_lds_b128(record, off + static_cast<std::uint32_t>(((hl * R + row) * C + logical * 8) * 2),
+                    lds_address(&dst[hl][row0 + j * kRpi][0]));
     }
-  }
-  __device__ __forceinline__ void load(const unsigned char *record, int c0) {
-    load_part(0, record, c0);
-    load_part(1, record, c0);
-    load_part(2, record, c0);
-  }
-  __device__ __forceinline__ void store(Scan3Shared &sh) const {
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int n = 0; n < 8; ++n) {
-      const int item = tid + 256 * n; // [2][64][16 pieces]
-      const int hl = item >> 10, row = (item >> 4) & 63, c = 8 * (item & 15);
-      *reinterpret_cast<u32x4 *>(&sh.w[hl][row][c]) = w[n];
-      if (n < kQK) *reinterpret_cast<u32x4 *>(&sh.q[hl][row][c]) = q[n];
-    }
-#pragma unroll
-    for (int n = 0; n < kQK; ++n) {
-      const int item = tid + 256 * n; // [2][128][8 pieces]
-      const int hl = item >> 10, row = (item >> 3) & 127, c = 8 * (item & 7);
-      *reinterpret_cast<u32x4 *>(&sh.kt[hl][row][c]) = kt[n];
-    }
-#pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      const int item = tid + 256 * n; // [2][64][8 pieces]
-      const int hl = item >> 9, row = (item >> 3) & 63, c = 8 * (item & 7);
-      *reinterpret_cast<u32x4 *>(&sh.m[hl][row][c]) = m[n];
-    }
-    if (tid < kChunk) sh.g[tid] = g;
-  }
-};
+}
 
 // Writes a C-layout 16x16 fp32 tile transposed and split: lane holds rows
 // 4*(lane/16) + r of column lane%16, stored at dst[col][row0 + 4*(lane/16) ..].
@@ -1173,22 +1143,62 @@ __device__ __forceinline__ void store_split_t(bf16_bits (*hi)[LD], bf16_bits (*l
   *reinterpret_cast<u32x2 *>(&lo[c][rr]) = u32x2{l0, l1};
 }
 
+// Loads of chunk record `record`, in the order the scan consumes them, each
+// wave fetching only the rows it reads.  The first part (W, U, G) has
+// kFirstLoads instructions per wave, K^T kKtLoads, Q and M kQmLoads.
+template <bool kExact> struct ScanLoads {
+  static constexpr int kQkHalves = kExact ? 1 : 2; // bf16 q / k inputs have no low part
+  static constexpr int kFirstLoads = 8 + 1 + 1;
+  static constexpr int kKtLoads = 4 * kQkHalves;
+  static constexpr int kQmLoads = 4 * kQkHalves + 4;
+  __device__ static void first(Scan3Shared &sh, const unsigned char *record, int wave, int c0,
+                               int parity) {
+    load_rows_lds<kChunk, kChunkDim, 16, 2>(record, rec::kW, sh.w, 16 * wave);
+    const int lane = threadIdx.x & 63;
+    // U rows 16 wave + lane / 4, 16-byte piece lane % 4 of columns c0 ..
+    load_lds_b128(record,
+                  static_cast<std::uint32_t>(rec::kU + ((16 * wave + (lane >> 2)) * kChunkDim + c0) * 4 +
+                                             (lane & 3) * 16),
+                  lds_address(&sh.u[16 * wave][0]));
+    // G[16 wave .. +15]: lanes 0..3 only (every wave issues the instruction).
+    if (lane < 4)
+      load_lds_b128(record, static_cast<std::uint32_t>(rec::kG + (16 * wave + 4 * lane) * 4),
+                    lds_address(&sh.g[parity][16 * wave]));
+  }
+  __device__ static void kt(Scan3Shared &sh, const unsigned char *record, int wave) {
+    load_rows_lds<kChunkDim, kChunk, 32, kQkHalves>(record, rec::kKt, sh.kt, 32 * wave);
+  }
+  __device__ static void qm(Scan3Shared &sh, const unsigned char *record, int wave) {
+    load_rows_lds<kChunk, kChunkDim, 16, kQkHalves>(record, rec::kQ, sh.q, 16 * wave);
+    load_rows_lds<kChunk, kChunk, 16, 2>(record, rec::kM, sh.m, 16 * wave);
+  }
+};
+
 // Block (value head, 16-column block), sequential over chunks.  Wave w owns
-// rows 16w.. of D and O and state rows 32w.. (two 16-row tiles) of S.
+// rows 16w.. of D and O and state rows 32w.. (two 16-row tiles) of S.  The
+// next chunk's record streams into LDS behind the current chunk's work: each
+// part is reissued as soon as its wave has finished reading the current one
+// (W, U, G after D; K^T after the S update; Q, M after O).
 template <bool kExact, typename OutT>
 __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
                                                          float *__restrict__ state,
                                                          OutT *__restrict__ out, std::size_t tokens,
                                                          std::size_t hv, float q_scale,
                                                          float k_scale) {
+  using Loads = ScanLoads<kExact>;
   __shared__ Scan3Shared sh;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15, lk = lane >> 4;
   const std::size_t h = blockIdx.x;
   const int c0 = blockIdx.y * kColBlock;
   float *sg = state + h * kChunkDim * kChunkDim;
-  ScanRegs<kExact> regs;
-  regs.load(scratch.at(h, 0), c0);
+  {
+    const unsigned char *first = scratch.at(h, 0);
+    Loads::first(sh, first, wave, c0, 0);
+    Loads::kt(sh, first, wave);
+    Loads::qm(sh, first, wave);
+  }
   // fp32 state tiles: s[tt] holds S[32 wave + 16 tt + 4 lk + r][c0 + lr].
   floatx4 s[2];
 #pragma unroll
@@ -1198,66 +1208,49 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) store_split_t<kLdK>(sh.st[0], sh.st[1], 32 * wave + 16 * tt, s[tt]);
 
+  const bf16_bits *w_hi = &sh.w[0][0][0], *w_lo = &sh.w[1][0][0];
+  const bf16_bits *q_hi = &sh.q[0][0][0], *q_lo = &sh.q[1][0][0];
+  const bf16_bits *kt_hi = &sh.kt[0][0][0], *kt_lo = &sh.kt[1][0][0];
+  const bf16_bits *m_hi = &sh.m[0][0][0], *m_lo = &sh.m[1][0][0];
+  const int i0 = 16 * wave;
   for (std::size_t c = 0, t0 = 0; t0 < tokens; ++c, t0 += kChunk) {
     const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
-    regs.store(sh);
-    const floatx4 u = regs.u;
-    __syncthreads(); // chunk operands and S^T in LDS
+    const int parity = static_cast<int>(c & 1);
     const bool more = t0 + kChunk < tokens;
     const unsigned char *next = scratch.at(h, more ? c + 1 : c);
-    if (more) regs.load_part(0, next, c0);
-    const int i0 = 16 * wave;
-    const float glast = sh.g[kChunk - 1]; // = G[L-1] (padded)
+    wait_vm<Loads::kQmLoads>(); // this chunk's W, U, G and K^T (Q, M may be in flight)
+    __syncthreads();            // G of every wave and S^T in LDS
+    const float *g = sh.g[parity];
+    const float glast = g[kChunk - 1]; // = G[L-1] (padded)
+    floatx4 u;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) u[r] = sh.u[i0 + 4 * lk + r][lr];
     // D = U - W S for rows i0 .. i0+15 (S^T is the B operand), and
     // D~ = e^{G_last - G} D for the S update (rows past L get weight 0).
     {
       floatx4 acc = floatx4{};
 #pragma unroll
       for (int kk = 0; kk < kChunkDim; kk += 32) {
-        const int ka = kk + 8 * lk;
-        acc = mfma_bf16(&sh.w[0][i0 + lr][ka], &sh.st[0][lr][ka], acc);
-        acc = mfma_bf16(&sh.w[0][i0 + lr][ka], &sh.st[1][lr][ka], acc);
-        acc = mfma_bf16(&sh.w[1][i0 + lr][ka], &sh.st[0][lr][ka], acc);
+        const int ka = kk + 8 * lk, wa = swz128(i0 + lr, kk / 8 + lk);
+        acc = mfma_bf16(w_hi + wa, &sh.st[0][lr][ka], acc);
+        acc = mfma_bf16(w_hi + wa, &sh.st[1][lr][ka], acc);
+        acc = mfma_bf16(w_lo + wa, &sh.st[0][lr][ka], acc);
       }
       floatx4 dv, fv;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = i0 + 4 * lk + r;
         dv[r] = u[r] - acc[r];
-        fv[r] = i < L ? __expf(glast - sh.g[i]) * dv[r] : 0.f;
+        fv[r] = i < L ? __expf(glast - g[i]) * dv[r] : 0.f;
       }
       store_split_t<kLdJ>(sh.dt[0], sh.dt[1], i0, dv);
       store_split_t<kLdJ>(sh.ft[0], sh.ft[1], i0, fv);
     }
+    wait_lgkm0(); // this wave's reads of W and U are done
+    if (more) Loads::first(sh, next, wave, c0, parity ^ 1);
     __syncthreads(); // D^T and D~^T of every row tile written
-    if (more) regs.load_part(1, next, c0);
-    // O = e^G (Q S) + M D for rows i0 .. i0+15 (q_scale is 1 unless Q is raw bf16).
-    {
-      floatx4 qa = floatx4{}, ma = floatx4{};
-#pragma unroll
-      for (int kk = 0; kk < kChunkDim; kk += 32) {
-        const int ka = kk + 8 * lk;
-        qa = mfma_bf16(&sh.q[0][i0 + lr][ka], &sh.st[0][lr][ka], qa);
-        qa = mfma_bf16(&sh.q[0][i0 + lr][ka], &sh.st[1][lr][ka], qa);
-        if constexpr (!kExact) qa = mfma_bf16(&sh.q[1][i0 + lr][ka], &sh.st[0][lr][ka], qa);
-      }
-#pragma unroll
-      for (int jj = 0; jj < kChunk; jj += 32) {
-        const int ja = jj + 8 * lk;
-        ma = mfma_bf16(&sh.m[0][i0 + lr][ja], &sh.dt[0][lr][ja], ma);
-        ma = mfma_bf16(&sh.m[0][i0 + lr][ja], &sh.dt[1][lr][ja], ma);
-        ma = mfma_bf16(&sh.m[1][i0 + lr][ja], &sh.dt[0][lr][ja], ma);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = i0 + 4 * lk + r;
-        if (i < L)
-          Elem<OutT>::store(out, ((t0 + i) * hv + h) * kChunkDim + c0 + lr,
-                            fmaf(__expf(sh.g[i]) * q_scale, qa[r], ma[r]));
-      }
-    }
-    if (more) regs.load_part(2, next, c0);
-    // S'[d][c] = e^{G_last} S[d][c] + sum_j K[j][d] D~[j][c], rows 32 wave + 16 tt.
+    // S'[d][c] = e^{G_last} S[d][c] + sum_j K[j][d] D~[j][c], rows 32 wave + 16 tt
+    // (registers only: S^T in LDS keeps the old state for O).
     const float egl = __expf(glast);
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
@@ -1265,15 +1258,49 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
       floatx4 acc = floatx4{};
 #pragma unroll
       for (int jj = 0; jj < kChunk; jj += 32) {
-        const int ja = jj + 8 * lk;
-        acc = mfma_bf16(&sh.kt[0][d0 + lr][ja], &sh.ft[0][lr][ja], acc);
-        acc = mfma_bf16(&sh.kt[0][d0 + lr][ja], &sh.ft[1][lr][ja], acc);
-        if constexpr (!kExact) acc = mfma_bf16(&sh.kt[1][d0 + lr][ja], &sh.ft[0][lr][ja], acc);
+        const int ja = jj + 8 * lk, ka = swz64(d0 + lr, jj / 8 + lk);
+        acc = mfma_bf16(kt_hi + ka, &sh.ft[0][lr][ja], acc);
+        acc = mfma_bf16(kt_hi + ka, &sh.ft[1][lr][ja], acc);
+        if constexpr (!kExact) acc = mfma_bf16(kt_lo + ka, &sh.ft[0][lr][ja], acc);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) s[tt][r] = fmaf(egl, s[tt][r], k_scale * acc[r]);
     }
-    __syncthreads(); // every wave is done reading S^T and this chunk's operands
+    wait_lgkm0(); // this wave's reads of K^T are done
+    if (more) {
+      Loads::kt(sh, next, wave);
+      wait_vm<Loads::kFirstLoads + Loads::kKtLoads>(); // this chunk's Q and M
+    } else {
+      wait_vm<0>();
+    }
+    // O = e^G (Q S) + M D for rows i0 .. i0+15 (q_scale is 1 unless Q is raw bf16).
+    {
+      floatx4 qa = floatx4{}, ma = floatx4{};
+#pragma unroll
+      for (int kk = 0; kk < kChunkDim; kk += 32) {
+        const int ka = kk + 8 * lk, qo = swz128(i0 + lr, kk / 8 + lk);
+        qa = mfma_bf16(q_hi + qo, &sh.st[0][lr][ka], qa);
+        qa = mfma_bf16(q_hi + qo, &sh.st[1][lr][ka], qa);
+        if constexpr (!kExact) qa = mfma_bf16(q_lo + qo, &sh.st[0][lr][ka], qa);
+      }
+#pragma unroll
+      for (int jj = 0; jj < kChunk; jj += 32) {
+        const int ja = jj + 8 * lk, mo = swz64(i0 + lr, jj / 8 + lk);
+        ma = mfma_bf16(m_hi + mo, &sh.dt[0][lr][ja], ma);
+        ma = mfma_bf16(m_hi + mo, &sh.dt[1][lr][ja], ma);
+        ma = mfma_bf16(m_lo + mo, &sh.dt[0][lr][ja], ma);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = i0 + 4 * lk + r;
+        if (i < L)
+          Elem<OutT>::store(out, ((t0 + i) * hv + h) * kChunkDim + c0 + lr,
+                            fmaf(__expf(g[i]) * q_scale, qa[r], ma[r]));
+      }
+    }
+    wait_lgkm0(); // this wave's reads of Q and M are done
+    if (more) Loads::qm(sh, next, wave);
+    __syncthreads(); // every wave is done reading S^T, D^T and D~^T
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) store_split_t<kLdK>(sh.st[0], sh.st[1], 32 * wave + 16 * tt, s[tt]);
   }
