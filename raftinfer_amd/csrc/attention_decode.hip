@@ -747,27 +747,31 @@ __global__ __launch_bounds__(256) void batched_append_kernel(const ActT *__restr
   cache[plane + idx] = f32_to_bf16(Elem<ActT>::load(value, src));
 }
 
+// Workgroup = (head, block of kMergeDims dims) of one sequence; thread = dim.
+// Chunks of 64 partitions: a 32768-token context (128 partitions) takes two
+// round trips.
 template <typename ActT>
-__global__ __launch_bounds__(256) void batched_merge_kernel(
+__global__ __launch_bounds__(kMergeDims) void batched_merge_kernel(
     const ActT *__restrict__ gate, ActT *__restrict__ output, const float *__restrict__ pmax,
     const float *__restrict__ psum, const float *__restrict__ pval,
     const std::uint32_t *__restrict__ lengths, std::size_t max_ctx, std::size_t max_partitions,
     std::size_t single_max) {
   const std::size_t seq = blockIdx.y;
-  const std::size_t head = blockIdx.x;
+  const std::size_t head = blockIdx.x / (kHeadDim / kMergeDims);
+  const int d = static_cast<int>(blockIdx.x % (kHeadDim / kMergeDims)) * kMergeDims + threadIdx.x;
   const std::size_t ctx = lengths[seq];
   if (ctx == 0 || ctx > max_ctx || ctx <= single_max) return;
   const std::size_t active = ctx / kBatchedPartition + (ctx % kBatchedPartition ? 1 : 0);
-  const std::size_t out_idx = (seq * kQueryHeads + head) * kHeadDim + threadIdx.x;
+  const std::size_t out_idx = (seq * kQueryHeads + head) * kHeadDim + d;
   const float gv = Elem<ActT>::load(gate, out_idx);
   float l, a;
-  merge_head(static_cast<int>(threadIdx.x), pmax, psum, pval, (seq * kQueryHeads + head) * max_partitions,
-             active, l, a);
+  merge_head<kMergeChunkLong>(d, pmax, psum, pval, (seq * kQueryHeads + head) * max_partitions,
+                              active, l, a);
   Elem<ActT>::store(output, out_idx, (a / l) * sigmoid_gate(gv));
 }
 
 // bf16 batched path: MFMA scores, dims-sliced workgroups, fused append.
-template <int DS, int WAVES>
+template <int DS, int WAVES, int CT>
 __global__ __launch_bounds__(WAVES * 64) void batched_mfma_kernel(
     const bf16_bits *__restrict__ query, const bf16_bits *__restrict__ key,
     const bf16_bits *__restrict__ value, const bf16_bits *__restrict__ gate,
@@ -775,7 +779,7 @@ __global__ __launch_bounds__(WAVES * 64) void batched_mfma_kernel(
     std::size_t max_ctx, const std::uint32_t *__restrict__ lengths, std::size_t max_partitions,
     std::size_t single_max, float *__restrict__ pmax, float *__restrict__ psum,
     float *__restrict__ pval) {
-  __shared__ DecodeMfmaShared<DS, WAVES> sh;
+  __shared__ DecodeMfmaShared<DS, WAVES, CT> sh;
   constexpr int DIMS = kHeadDim / DS;
   const std::size_t seq = blockIdx.y;
   const std::size_t ctx = lengths[seq];
@@ -800,7 +804,7 @@ __global__ __launch_bounds__(WAVES * 64) void batched_mfma_kernel(
   const DecodeMfmaArgs a{query + seq * kQueryHeads * kHeadDim, key + seq * kKvHeads * kHeadDim,
                          value + seq * kKvHeads * kHeadDim, cache, cache, max_ctx, true};
   const std::size_t pos = ctx - 1;
-  decode_mfma_scan<DS, WAVES>(a, kv_head, dq, begin, end, pos, sh);
+  decode_mfma_scan<DS, WAVES, CT>(a, kv_head, dq, begin, end, pos, sh);
   __syncthreads();
   if (dq == 0 && pos >= begin && pos < end) append_rows(a, kv_head, pos);
   for (int o = threadIdx.x; o < kGroup * DIMS; o += WAVES * 64) {
@@ -839,13 +843,15 @@ void launch_batched(const void *query, const void *key, const void *value, const
   auto *out = static_cast<ActT *>(output);
   const unsigned int seqs = static_cast<unsigned int>(shape.sequences);
   if constexpr (std::is_same_v<ActT, bf16_bits>) {
-    constexpr int DS = 1, WAVES = 8;
-    batched_mfma_kernel<DS, WAVES>
+    // 4-wave workgroups: two fit a CU (218 VGPRs, two waves per SIMD), so one
+    // workgroup's loads overlap the other's reduction and stores.
+    constexpr int DS = 1, WAVES = 4, CT = 32;
+    batched_mfma_kernel<DS, WAVES, CT>
         <<<dim3(xcd_grid<DS>(kKvHeads * max_partitions), seqs), WAVES * 64, 0, stream>>>(
             q, k, v, g, out, base, shape.cache_stride_bytes, shape.max_context_tokens, lengths,
             max_partitions, shape.single_block_max_tokens, pmax, psum, pval);
     check_launch<Err>("qwen35_batched_decode_partition");
-    batched_merge_kernel<ActT><<<dim3(kQueryHeads, seqs), 256, 0, stream>>>(
+    batched_merge_kernel<ActT><<<dim3(kQueryHeads * (kHeadDim / kMergeDims), seqs), kMergeDims, 0, stream>>>(
         g, out, pmax, psum, pval, lengths, shape.max_context_tokens, max_partitions,
         shape.single_block_max_tokens);
     check_launch<Err>("qwen35_batched_decode_merge");
@@ -860,7 +866,7 @@ void launch_batched(const void *query, const void *key, const void *value, const
       q, k, v, g, out, base, shape.cache_stride_bytes, shape.max_context_tokens, lengths,
       max_partitions, shape.single_block_max_tokens, pmax, psum, pval);
   check_launch<Err>("qwen35_batched_decode_partition");
-  batched_merge_kernel<ActT><<<dim3(kQueryHeads, seqs), 256, 0, stream>>>(
+  batched_merge_kernel<ActT><<<dim3(kQueryHeads * (kHeadDim / kMergeDims), seqs), kMergeDims, 0, stream>>>(
       g, out, pmax, psum, pval, lengths, shape.max_context_tokens, max_partitions,
       shape.single_block_max_tokens);
   check_launch<Err>("qwen35_batched_decode_merge");

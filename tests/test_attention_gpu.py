@@ -287,10 +287,14 @@ def test_materialized_path(gpu, act, T, past):
     assert close_enough(from_dev(out).reshape(T, hq, d), expect)
 
 
-def test_batched_ragged_decode(gpu):
+@pytest.mark.parametrize("lengths,max_ctx", [
+    ([1, 100, 511, 512, 513, 777, 2000, 4096], 4096),
+    # 66 partitions: the merge takes a second chunk of partials.
+    ([16641, 700], 16896),
+])
+def test_batched_ragged_decode(gpu, lengths, max_ctx):
     # BASELINE config 4 at reduced length: per-sequence oracle, mixed policies.
-    lengths = [1, 100, 511, 512, 513, 777, 2000, 4096]
-    B, max_ctx = len(lengths), 4096
+    B = len(lengths)
     r = rng(77)
     per = 2 * max_ctx * HKV * D
     cache_np = np.zeros(B * per, np.float32)
