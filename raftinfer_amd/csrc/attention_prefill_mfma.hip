@@ -29,8 +29,10 @@
 //               of one dim), eight MFMAs' operands at a time.  The O^T
 //               accumulators stay in AGPRs (inline-asm MFMA).
 // The waves' partial (max, sum, O) are merged through LDS at the end; wave w
-// finishes dims [64w, 64w+64) and applies the sigmoid gate, whose loads were
-// issued at the start.  With past == 0 the keys come from the key/value
+// finishes dims [64w, 64w+64) and applies the sigmoid gate.  The gate is
+// loaded at the start as whole 16-byte row pieces and the output stored the
+// same way, both staged through the Q area of LDS, so neither goes out as
+// scattered 8-byte pieces.  With past == 0 the keys come from the key/value
 // inputs and each workgroup also writes its 8 tokens' cache rows (the append).
 #include "decode_scan.hpp"
 #include "prefill_mfma.hpp"
@@ -71,6 +73,10 @@ __device__ __forceinline__ int swz(int r) { return r & 7; }
 __device__ __forceinline__ int chunk_offset(int r, int c) { // in bf16 elements
   return r * kHeadDim + ((c ^ swz(r)) << 3);
 }
+
+// Gate / output staging in the Q area: element offset of 16-byte chunk k of
+// column row c.
+__device__ __forceinline__ int io_offset(int c, int k) { return c * kHeadDim + ((k ^ (c & 31)) << 3); }
 
 __device__ __forceinline__ bf16x8 lds_b128(const bf16_bits *p) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(p));
@@ -214,19 +220,19 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
       app[j] = *reinterpret_cast<const u32x4 *>(src + 8 * piece);
     }
   }
-  // Gate loads for this wave's output quarter (dims 64 wave .. +63) go out
-  // first: they are needed only in the epilogue, so the whole tile loop hides
-  // their latency.
-  // Register i of O^T block nb holds dim 32 nb + 8 (i / 4) + 4 half + i % 4.
-  const bool col_live = static_cast<std::size_t>(col_tok) < q_rows;
-  const std::size_t out_row = ((t0 + col_row) * kQueryHeads + col_head) * kHeadDim;
-  u32x2 gv[2][4];
+  // Gate rows of this workgroup, loaded first and held in registers until the
+  // epilogue: token tt's four heads are 2 KiB contiguous, read in 16-byte
+  // pieces (thread -> pieces tid + 256 j: token idx >> 7, piece idx & 127), so
+  // each load instruction covers whole 128-byte lines.
+  const std::size_t io_base = (t0 * kQueryHeads + kv_head * kGroup) * kHeadDim;
+  u32x4 gc[4];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4)
-      gv[j][i4] = *reinterpret_cast<const u32x2 *>(gate + out_row + 32 * (2 * wave + j) + 8 * i4 +
-                                                   4 * half);
+  for (int j = 0; j < 4; ++j) {
+    const int idx = tid + kThreads * j, tt = idx >> 7, piece = idx & 127;
+    gc[j] = u32x4{0u, 0u, 0u, 0u};
+    if (static_cast<std::size_t>(tt) < q_rows)
+      gc[j] = *reinterpret_cast<const u32x4 *>(gate + io_base + tt * kQueryHeads * kHeadDim + 8 * piece);
+  }
   // Q tile -> LDS, row = column c (token c % 8 of head 4 kv + c / 8), in the
   // K tile's chunk order; wave w loads rows 8w .. 8w+7 (4 instructions).
   {
@@ -255,6 +261,7 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
   for (; t < n_tiles; t += kWaves) {
     const std::size_t k0 = t * kKTile;
     const bool more = t + kWaves < n_tiles;
+    const std::size_t k0_next = k0 + kWaves * kKTile;
     wait_vm<16>(); // K(t) has landed; V(t) may still be in flight
     // S^T = K Q^T: A row = key `col` of the tile (lane & 31), k-half `half`.
     // Chunk 2 kb + half of row `col` sits at (2 (kb & 3) + half) ^ (col & 7)
@@ -273,7 +280,7 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
       for (int j = 0; j < 4; ++j) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[j], qa[j], s, 0, 0, 0);
     }
     wait_lgkm0(); // the K tile has been read
-    if (more) issue(k_src, lds_k, k0 + kWaves * kKTile);
+    if (more) issue(k_src, lds_k, k0_next);
 
     // Key of accumulator register i: k0 + 8 (i / 4) + 4 half + i % 4.  Only
     // a tile that reaches past the tile's first query position is masked.
@@ -352,11 +359,20 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
       mfma_drain(); // the accumulators may be read by VALU code below
     }
     wait_lgkm0(); // the V tile has been read
-    if (more) issue(v_src, lds_v, k0 + kWaves * kKTile);
+    if (more) issue(v_src, lds_v, k0_next);
   }
 
 
-  __syncthreads(); // every wave is done with its tile
+  __syncthreads(); // every wave is done with its tile (and with Q)
+  // The gate goes to the Q area as [column][256] rows, 16-byte chunk k of row
+  // c at k ^ (c & 31): the epilogue's 8-byte reads (32 rows, one chunk) then
+  // hit distinct banks.
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int idx = tid + kThreads * j, tt = idx >> 7, piece = idx & 127;
+    const int c = (piece >> 5) * kQTok + tt;
+    *reinterpret_cast<u32x4 *>(sh.q + io_offset(c, piece & 31)) = gc[j];
+  }
   // Wave w finishes O^T blocks 2w, 2w+1 (dims 64w .. 64w+63): it hands the
   // other three quarters over through LDS and keeps its own in registers.
   // (The quarter loop is unrolled so that every register index is a
@@ -411,19 +427,27 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
       }
   }
   const float inv = 1.0f / (lsum + xor32(lsum));
-  if (col_live) {
+  // Gated outputs replace the gate in LDS (each lane rewrites exactly the
+  // 8-byte pieces it read), then go out as whole 16-byte row pieces.
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const u32x2 g = gv[j][i4];
-        const floatx16 &x = f[j];
-        const u32x2 w{pack_bf16x2(x[4 * i4] * inv * sigmoid_gate(bf16_lo(g[0])),
-                                  x[4 * i4 + 1] * inv * sigmoid_gate(bf16_hi(g[0]))),
-                      pack_bf16x2(x[4 * i4 + 2] * inv * sigmoid_gate(bf16_lo(g[1])),
-                                  x[4 * i4 + 3] * inv * sigmoid_gate(bf16_hi(g[1])))};
-        *reinterpret_cast<u32x2 *>(output + out_row + 32 * (2 * wave + j) + 8 * i4 + 4 * half) = w;
-      }
+    for (int i4 = 0; i4 < 4; ++i4) {
+      auto *slot = reinterpret_cast<u32x2 *>(sh.q + io_offset(col, 4 * (2 * wave + j) + i4) + 4 * half);
+      const u32x2 g = *slot;
+      const floatx16 &x = f[j];
+      *slot = u32x2{pack_bf16x2(x[4 * i4] * inv * sigmoid_gate(bf16_lo(g[0])),
+                                x[4 * i4 + 1] * inv * sigmoid_gate(bf16_hi(g[0]))),
+                    pack_bf16x2(x[4 * i4 + 2] * inv * sigmoid_gate(bf16_lo(g[1])),
+                                x[4 * i4 + 3] * inv * sigmoid_gate(bf16_hi(g[1])))};
+    }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int idx = tid + kThreads * j, tt = idx >> 7, piece = idx & 127;
+    if (static_cast<std::size_t>(tt) < q_rows)
+      *reinterpret_cast<u32x4 *>(output + io_base + tt * kQueryHeads * kHeadDim + 8 * piece) =
+          *reinterpret_cast<const u32x4 *>(sh.q + io_offset((piece >> 5) * kQTok + tt, piece & 31));
   }
   if constexpr (FromInput) {
 #pragma unroll
