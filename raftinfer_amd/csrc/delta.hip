@@ -979,14 +979,31 @@ __global__ __launch_bounds__(256) void chunk_prep_bf16_kernel(Src<bf16_bits> qs,
   __syncthreads();
   {
     bf16_bits *kr = reinterpret_cast<bf16_bits *>(record + rec::kKt);
-    for (int item = tid; item < kChunkDim * (kChunk / 8); item += 256) {
-      const int d = item >> 3, j = 8 * (item & 7);
-      *reinterpret_cast<u32x4 *>(kr + d * kChunk + j) = *reinterpret_cast<const u32x4 *>(&sh.kt[d][j]);
+    u32x4 kv[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const int item = tid + 256 * n, d = item >> 3, j = 8 * (item & 7);
+      kv[n] = *reinterpret_cast<const u32x4 *>(&sh.kt[d][j]);
+    }
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const int item = tid + 256 * n, d = item >> 3, j = 8 * (item & 7);
+      *reinterpret_cast<u32x4 *>(kr + d * kChunk + j) = kv[n];
     }
   }
   // M = e^{G_i-G_j} (q_i . k_j) q_scale k_scale (j <= i), A = beta_i e^{G_i-G_j}
   // (k_i . k_j) k_scale^2 (j < i); wave w = row tile w, exact bf16 products.
   const float qk_scale = qs.scale * ks.scale, kk_scale = ks.scale * ks.scale;
+  // Per-lane decay and beta values, read once: rows i = 16 wave + 4 lk + r,
+  // columns j = 16 tj + lr.
+  float gi[4], bi[4], gj[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    gi[r] = sh.g[wave * 16 + lk * 4 + r];
+    bi[r] = sh.beta[wave * 16 + lk * 4 + r] * kk_scale;
+    gj[r] = sh.g[r * 16 + lr];
+  }
+#pragma unroll
   for (int tj = 0; tj < 4; ++tj) {
     floatx4 am = floatx4{}, aa = floatx4{};
     if (tj <= wave) {
@@ -1000,25 +1017,35 @@ __global__ __launch_bounds__(256) void chunk_prep_bf16_kernel(Src<bf16_bits> qs,
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = wave * 16 + lk * 4 + r, j = tj * 16 + lr;
-      const float e = __expf(sh.g[i] - sh.g[j]);
+      const float e = __expf(gi[r] - gj[tj]);
       sh.mm[i][j] = (j <= i && i < L) ? am[r] * qk_scale * e : 0.f;
-      sh.r3.at.a[i][j] = (j < i && i < L) ? sh.beta[i] * e * aa[r] * kk_scale : 0.f;
+      sh.r3.at.a[i][j] = (j < i && i < L) ? bi[r] * e * aa[r] : 0.f;
     }
   }
   __syncthreads();
   invert_unit_lower_64(sh.r3.at.a, sh.r3.at.tm, sh.r1.y);
   // tw = T diag(beta e^G k_scale), tu = T diag(beta v_scale), split.
-  for (int item = tid; item < kChunk * (kChunk / 2); item += 256) {
-    const int i = item >> 5, j = 2 * (item & 31);
-    const float t0v = sh.r3.at.tm[i][j], t1v = sh.r3.at.tm[i][j + 1];
+  // Thread -> column pair j = 2 (tid % 32), rows tid / 32 + 8 n: the column
+  // factors are read once and the eight row pairs in one batch.
+  {
+    const int j = 2 * (tid & 31), i0 = tid >> 5;
     const float b0 = sh.beta[j], b1 = sh.beta[j + 1];
-    std::uint32_t hi, lo;
-    split2(t0v * b0 * __expf(sh.g[j]) * ks.scale, t1v * b1 * __expf(sh.g[j + 1]) * ks.scale, hi, lo);
-    *reinterpret_cast<std::uint32_t *>(&sh.tw[0][i][j]) = hi;
-    *reinterpret_cast<std::uint32_t *>(&sh.tw[1][i][j]) = lo;
-    split2(t0v * b0 * vs.scale, t1v * b1 * vs.scale, hi, lo);
-    *reinterpret_cast<std::uint32_t *>(&sh.tu[0][i][j]) = hi;
-    *reinterpret_cast<std::uint32_t *>(&sh.tu[1][i][j]) = lo;
+    const float fw0 = b0 * __expf(sh.g[j]) * ks.scale, fw1 = b1 * __expf(sh.g[j + 1]) * ks.scale;
+    const float fu0 = b0 * vs.scale, fu1 = b1 * vs.scale;
+    float2 tv[8];
+#pragma unroll
+    for (int n = 0; n < 8; ++n) tv[n] = *reinterpret_cast<const float2 *>(&sh.r3.at.tm[i0 + 8 * n][j]);
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const int i = i0 + 8 * n;
+      std::uint32_t hi, lo;
+      split2(tv[n].x * fw0, tv[n].y * fw1, hi, lo);
+      *reinterpret_cast<std::uint32_t *>(&sh.tw[0][i][j]) = hi;
+      *reinterpret_cast<std::uint32_t *>(&sh.tw[1][i][j]) = lo;
+      split2(tv[n].x * fu0, tv[n].y * fu1, hi, lo);
+      *reinterpret_cast<std::uint32_t *>(&sh.tu[0][i][j]) = hi;
+      *reinterpret_cast<std::uint32_t *>(&sh.tu[1][i][j]) = lo;
+    }
   }
   __syncthreads();
   // W = tw K, U = tu V (B operands K^T, V^T): 4 x 8 tiles, wave w takes w + 4n.
