@@ -645,10 +645,12 @@ __device__ __forceinline__ void invert_unit_lower_64(const float (*a)[kLdC], flo
 #pragma unroll
         for (int j = 0; j < r; ++j) c[r][j] = a[b + r][b + j];
       }
+      // Right-looking: once x[j] is final, the updates of rows j+1.. are
+      // independent, so the dependent chain is 15 FMAs long, not 120.
 #pragma unroll
-      for (int r = 1; r < 16; ++r)
+      for (int j = 0; j < 15; ++j)
 #pragma unroll
-        for (int j = 0; j < r; ++j) x[r] = fmaf(-c[r][j], x[j], x[r]);
+        for (int r = j + 1; r < 16; ++r) x[r] = fmaf(-c[r][j], x[j], x[r]);
 #pragma unroll
       for (int r = 0; r < 16; ++r) tm[b + r][b + lane] = x[r];
     }
@@ -676,17 +678,32 @@ __device__ __forceinline__ void invert_unit_lower_64(const float (*a)[kLdC], flo
   // 3. Lower-left 32 x 32 block = -T_BR A_BL T_TL; wave w -> tile (2 + w/2, w%2).
   const int ti = 2 + (wave >> 1), tj = wave & 1;
   {
+    // T_TL is lower triangular and its upper right block is stored as 0, so
+    // the full k range gives the same sums; the operands are read up front.
+    float av[8], bv[8];
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      av[n] = a[16 * ti + lr][4 * n + lk];
+      bv[n] = tm[4 * n + lk][16 * tj + lr];
+    }
     floatx4 acc = floatx4{};
-    for (int k0 = 16 * tj; k0 < 32; k0 += 4) // T_TL is lower triangular
-      acc = mfma4(a[16 * ti + lr][k0 + lk], tm[k0 + lk][16 * tj + lr], acc);
+#pragma unroll
+    for (int n = 0; n < 8; ++n) acc = mfma4(av[n], bv[n], acc);
 #pragma unroll
     for (int r = 0; r < 4; ++r) y[16 * (ti - 2) + 4 * lk + r][16 * tj + lr] = acc[r];
   }
   __syncthreads();
   {
+    // T_BR is lower triangular with its upper right block stored as 0.
+    float av[8], bv[8];
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      av[n] = tm[16 * ti + lr][32 + 4 * n + lk];
+      bv[n] = y[4 * n + lk][16 * tj + lr];
+    }
     floatx4 acc = floatx4{};
-    for (int k0 = 32; k0 < 16 * ti + 16; k0 += 4) // T_BR is lower triangular
-      acc = mfma4(tm[16 * ti + lr][k0 + lk], y[k0 - 32 + lk][16 * tj + lr], acc);
+#pragma unroll
+    for (int n = 0; n < 8; ++n) acc = mfma4(av[n], bv[n], acc);
 #pragma unroll
     for (int r = 0; r < 4; ++r) tm[16 * ti + 4 * lk + r][16 * tj + lr] = -acc[r];
   }
