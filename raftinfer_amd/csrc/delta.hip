@@ -919,6 +919,9 @@ struct PrepBShared {
   float beta[kChunk];
 };
 
+__device__ __forceinline__ bf16x8 lds8(const bf16_bits *p) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(p));
+}
 __device__ __forceinline__ floatx4 mfma_b(const bf16_bits *a, const bf16_bits *b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
       __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(a)),
@@ -1020,23 +1023,39 @@ __global__ __launch_bounds__(256) void chunk_prep_bf16_kernel(Src<bf16_bits> qs,
     bi[r] = sh.beta[wave * 16 + lk * 4 + r] * kk_scale;
     gj[r] = sh.g[r * 16 + lr];
   }
+  // Row operands (this wave's Q and K rows) are read once; each column tile's
+  // K rows are read before its eight products, and every product runs before
+  // any result is scaled, so LDS latency is paid about once per tile.
+  bf16x8 qrow[4], krow[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    qrow[kk] = lds8(&sh.r1.qk.q[wave * 16 + lr][32 * kk + 8 * lk]);
+    krow[kk] = lds8(&sh.r1.qk.k[wave * 16 + lr][32 * kk + 8 * lk]);
+  }
+  floatx4 am[4], aa[4];
 #pragma unroll
   for (int tj = 0; tj < 4; ++tj) {
-    floatx4 am = floatx4{}, aa = floatx4{};
+    am[tj] = floatx4{};
+    aa[tj] = floatx4{};
     if (tj <= wave) {
+      bf16x8 kcol[4];
 #pragma unroll
-      for (int kk = 0; kk < kChunkDim; kk += 32) {
-        const int ka = kk + 8 * lk;
-        am = mfma_b(&sh.r1.qk.q[wave * 16 + lr][ka], &sh.r1.qk.k[tj * 16 + lr][ka], am);
-        aa = mfma_b(&sh.r1.qk.k[wave * 16 + lr][ka], &sh.r1.qk.k[tj * 16 + lr][ka], aa);
+      for (int kk = 0; kk < 4; ++kk) kcol[kk] = lds8(&sh.r1.qk.k[tj * 16 + lr][32 * kk + 8 * lk]);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        am[tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qrow[kk], kcol[kk], am[tj], 0, 0, 0);
+        aa[tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(krow[kk], kcol[kk], aa[tj], 0, 0, 0);
       }
     }
+  }
+#pragma unroll
+  for (int tj = 0; tj < 4; ++tj) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = wave * 16 + lk * 4 + r, j = tj * 16 + lr;
       const float e = __expf(gi[r] - gj[tj]);
-      sh.mm[i][j] = (j <= i && i < L) ? am[r] * qk_scale * e : 0.f;
-      sh.r3.at.a[i][j] = (j < i && i < L) ? bi[r] * e * aa[r] : 0.f;
+      sh.mm[i][j] = (j <= i && i < L) ? am[tj][r] * qk_scale * e : 0.f;
+      sh.r3.at.a[i][j] = (j < i && i < L) ? bi[r] * e * aa[tj][r] : 0.f;
     }
   }
   __syncthreads();
@@ -1144,9 +1163,6 @@ struct Scan3Shared {
 __device__ __forceinline__ int swz128(int r, int c) { return r * kChunkDim + ((c ^ (r & 15)) << 3); }
 __device__ __forceinline__ int swz64(int r, int c) { return r * kChunk + ((c ^ ((r >> 1) & 7)) << 3); }
 
-__device__ __forceinline__ bf16x8 lds8(const bf16_bits *p) {
-  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(p));
-}
 __device__ __forceinline__ floatx4 mfma_bf16(const bf16_bits *a, const bf16_bits *b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(lds8(a), lds8(b), c, 0, 0, 0);
 }
