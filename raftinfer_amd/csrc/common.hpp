@@ -198,16 +198,27 @@ template <typename T> __device__ __forceinline__ unsigned lds_address(T *p) {
 }
 
 // 16 bytes from base + voff (per lane) into LDS at lds + 16 * lane
-// (global_load_lds_dwordx4).  Written as asm, with the waits below issued by
-// hand: the compiler cannot tell which LDS region such a load writes and
-// would otherwise wait for every outstanding one before each LDS read.  The
-// kernels that use it issue no other instruction that reads M0.
+// (global_load_lds_dwordx4).  base and lds must be wave-uniform; they are
+// moved to scalar registers here (readfirstlane), so the instruction's scalar
+// operands never depend on the compiler proving that uniformity.  Written as
+// asm, with the waits below issued by hand: the compiler cannot tell which
+// LDS region such a load writes and would otherwise wait for every
+// outstanding one before each LDS read.  The kernels that use it issue no
+// other instruction that reads M0.
 __device__ __forceinline__ void load_lds_b128(const void *base, std::uint32_t voff, unsigned lds) {
+  // readfirstlane returns int: each half goes back to uint32 before it is
+  // widened, so a low word with bit 31 set is not sign-extended into the
+  // high word.
+  const auto b = reinterpret_cast<std::uintptr_t>(base);
+  const auto hi = static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<std::uint32_t>(b >> 32)));
+  const auto lo = static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<std::uint32_t>(b)));
+  const std::uint64_t sbase = (static_cast<std::uint64_t>(hi) << 32) | lo;
+  const auto slds = static_cast<unsigned>(__builtin_amdgcn_readfirstlane(lds));
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
                :
-               : "s"(lds), "v"(voff), "s"(base)
+               : "s"(slds), "v"(voff), "s"(sbase)
                : "memory", "m0");
 #pragma clang diagnostic pop
 }
