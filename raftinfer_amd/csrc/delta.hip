@@ -1282,26 +1282,48 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
     __syncthreads();            // G of every wave and S^T in LDS
     const float *g = sh.g[parity];
     const float glast = g[kChunk - 1]; // = G[L-1] (padded)
-    floatx4 u;
+    // Per-row factors of this lane's rows i = i0 + 4 lk + r, computed before
+    // the products so the exponentials overlap the MFMA latency:
+    // e^{G_last - G_i} for D~ (0 past L) and e^{G_i} q_scale for O.
+    floatx4 u, fdec, eq;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) u[r] = sh.u[i0 + 4 * lk + r][lr];
+    for (int r = 0; r < 4; ++r) {
+      const int i = i0 + 4 * lk + r;
+      const float gi = g[i];
+      u[r] = sh.u[i][lr];
+      fdec[r] = i < L ? __expf(glast - gi) : 0.f;
+      eq[r] = __expf(gi) * q_scale;
+    }
     // D = U - W S for rows i0 .. i0+15 (S^T is the B operand), and
     // D~ = e^{G_last - G} D for the S update (rows past L get weight 0).
+    // Operands are read before any product, and the three hi/lo products
+    // accumulate separately (chains of 4 MFMAs instead of 12).
     {
-      floatx4 acc = floatx4{};
+      bf16x8 wh[4], wl[4], sth[4], stl[4];
 #pragma unroll
-      for (int kk = 0; kk < kChunkDim; kk += 32) {
-        const int ka = kk + 8 * lk, wa = swz128(i0 + lr, kk / 8 + lk);
-        acc = mfma_bf16(w_hi + wa, &sh.st[0][lr][ka], acc);
-        acc = mfma_bf16(w_hi + wa, &sh.st[1][lr][ka], acc);
-        acc = mfma_bf16(w_lo + wa, &sh.st[0][lr][ka], acc);
+      for (int n = 0; n < 4; ++n) {
+        const int ka = 32 * n + 8 * lk, wa = swz128(i0 + lr, 4 * n + lk);
+        wh[n] = lds8(w_hi + wa);
+        wl[n] = lds8(w_lo + wa);
+        sth[n] = lds8(&sh.st[0][lr][ka]);
+        stl[n] = lds8(&sh.st[1][lr][ka]);
       }
+      floatx4 a0 = floatx4{}, a1 = floatx4{}, a2 = floatx4{};
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wh[n], sth[n], a0, 0, 0, 0);
+        a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wh[n], stl[n], a1, 0, 0, 0);
+        a2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wl[n], sth[n], a2, 0, 0, 0);
+      }
+      floatx4 acc;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = a0[r] + (a1[r] + a2[r]);
       floatx4 dv, fv;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = i0 + 4 * lk + r;
         dv[r] = u[r] - acc[r];
-        fv[r] = i < L ? __expf(glast - g[i]) * dv[r] : 0.f;
+        fv[r] = fdec[r] * dv[r];
       }
       store_split_t<kLdJ>(sh.dt[0], sh.dt[1], i0, dv);
       store_split_t<kLdJ>(sh.ft[0], sh.ft[1], i0, fv);
@@ -1315,14 +1337,25 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       const int d0 = 32 * wave + 16 * tt;
-      floatx4 acc = floatx4{};
+      bf16x8 kh[2], kl[2], fh[2], fl[2];
 #pragma unroll
-      for (int jj = 0; jj < kChunk; jj += 32) {
-        const int ja = jj + 8 * lk, ka = swz64(d0 + lr, jj / 8 + lk);
-        acc = mfma_bf16(kt_hi + ka, &sh.ft[0][lr][ja], acc);
-        acc = mfma_bf16(kt_hi + ka, &sh.ft[1][lr][ja], acc);
-        if constexpr (!kExact) acc = mfma_bf16(kt_lo + ka, &sh.ft[0][lr][ja], acc);
+      for (int n = 0; n < 2; ++n) {
+        const int ja = 32 * n + 8 * lk, ka = swz64(d0 + lr, 4 * n + lk);
+        kh[n] = lds8(kt_hi + ka);
+        if constexpr (!kExact) kl[n] = lds8(kt_lo + ka);
+        fh[n] = lds8(&sh.ft[0][lr][ja]);
+        fl[n] = lds8(&sh.ft[1][lr][ja]);
       }
+      floatx4 s0 = floatx4{}, s1 = floatx4{}, s2 = floatx4{};
+#pragma unroll
+      for (int n = 0; n < 2; ++n) {
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh[n], fh[n], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh[n], fl[n], s1, 0, 0, 0);
+        if constexpr (!kExact) s2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl[n], fh[n], s2, 0, 0, 0);
+      }
+      floatx4 acc;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = s0[r] + (s1[r] + s2[r]);
 #pragma unroll
       for (int r = 0; r < 4; ++r) s[tt][r] = fmaf(egl, s[tt][r], k_scale * acc[r]);
     }
@@ -1335,27 +1368,47 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
     }
     // O = e^G (Q S) + M D for rows i0 .. i0+15 (q_scale is 1 unless Q is raw bf16).
     {
-      floatx4 qa = floatx4{}, ma = floatx4{};
+      bf16x8 qh[4], ql[4], sth[4], stl[4], mh[2], ml[2], dth[2], dtl[2];
 #pragma unroll
-      for (int kk = 0; kk < kChunkDim; kk += 32) {
-        const int ka = kk + 8 * lk, qo = swz128(i0 + lr, kk / 8 + lk);
-        qa = mfma_bf16(q_hi + qo, &sh.st[0][lr][ka], qa);
-        qa = mfma_bf16(q_hi + qo, &sh.st[1][lr][ka], qa);
-        if constexpr (!kExact) qa = mfma_bf16(q_lo + qo, &sh.st[0][lr][ka], qa);
+      for (int n = 0; n < 4; ++n) {
+        const int ka = 32 * n + 8 * lk, qo = swz128(i0 + lr, 4 * n + lk);
+        qh[n] = lds8(q_hi + qo);
+        if constexpr (!kExact) ql[n] = lds8(q_lo + qo);
+        sth[n] = lds8(&sh.st[0][lr][ka]);
+        stl[n] = lds8(&sh.st[1][lr][ka]);
       }
 #pragma unroll
-      for (int jj = 0; jj < kChunk; jj += 32) {
-        const int ja = jj + 8 * lk, mo = swz64(i0 + lr, jj / 8 + lk);
-        ma = mfma_bf16(m_hi + mo, &sh.dt[0][lr][ja], ma);
-        ma = mfma_bf16(m_hi + mo, &sh.dt[1][lr][ja], ma);
-        ma = mfma_bf16(m_lo + mo, &sh.dt[0][lr][ja], ma);
+      for (int n = 0; n < 2; ++n) {
+        const int ja = 32 * n + 8 * lk, mo = swz64(i0 + lr, 4 * n + lk);
+        mh[n] = lds8(m_hi + mo);
+        ml[n] = lds8(m_lo + mo);
+        dth[n] = lds8(&sh.dt[0][lr][ja]);
+        dtl[n] = lds8(&sh.dt[1][lr][ja]);
+      }
+      floatx4 q0 = floatx4{}, q1 = floatx4{}, q2 = floatx4{}, m0 = floatx4{}, m1 = floatx4{}, m2 = floatx4{};
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        q0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh[n], sth[n], q0, 0, 0, 0);
+        q1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh[n], stl[n], q1, 0, 0, 0);
+        if constexpr (!kExact) q2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql[n], sth[n], q2, 0, 0, 0);
+      }
+#pragma unroll
+      for (int n = 0; n < 2; ++n) {
+        m0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mh[n], dth[n], m0, 0, 0, 0);
+        m1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mh[n], dtl[n], m1, 0, 0, 0);
+        m2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ml[n], dth[n], m2, 0, 0, 0);
+      }
+      floatx4 qa, ma;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        qa[r] = q0[r] + (q1[r] + q2[r]);
+        ma[r] = m0[r] + (m1[r] + m2[r]);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = i0 + 4 * lk + r;
         if (i < L)
-          Elem<OutT>::store(out, ((t0 + i) * hv + h) * kChunkDim + c0 + lr,
-                            fmaf(__expf(g[i]) * q_scale, qa[r], ma[r]));
+          Elem<OutT>::store(out, ((t0 + i) * hv + h) * kChunkDim + c0 + lr, fmaf(eq[r], qa[r], ma[r]));
       }
     }
     wait_lgkm0(); // this wave's reads of Q and M are done
