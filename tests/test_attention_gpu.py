@@ -320,3 +320,46 @@ def test_batched_ragged_decode(gpu, lengths, max_ctx):
     got = from_dev(out)
     for b in range(B):
         assert_bf16_close(got[b], bf16(expects[b]), what=f"batched seq {b} len {lengths[b]}")
+
+
+def test_batched_ragged_decode_cfg4_full_size(gpu):
+    # BASELINE config 4 at full size: 32 sequences with lengths U{1..32768} from the bench's
+    # seed, max_ctx 32768, bf16 head-major caches (4.3 GB).  Every sequence is checked against
+    # the single-sequence decode entry point (pinned to the oracle by the tests above) on the
+    # same, already appended cache; the shortest, the longest and two others also against the
+    # C oracle directly.
+    lengths = np.random.default_rng(0x5241465449 + 4).integers(1, 32769, size=32)
+    B, max_ctx = len(lengths), 32768
+    per = 2 * HKV * max_ctx * D
+    gen = torch.Generator(device="cuda").manual_seed(44)
+    cache = torch.empty(B * per, device="cuda", dtype=torch.bfloat16)
+    for b in range(B):
+        cache[b * per:(b + 1) * per].copy_(torch.randn(per, device="cuda", generator=gen))
+    q, g = (torch.randn(B, HQ, D, device="cuda", generator=gen).to(torch.bfloat16) for _ in range(2))
+    k, v = (torch.randn(B, HKV, D, device="cuda", generator=gen).to(torch.bfloat16) for _ in range(2))
+    lens = torch.tensor(lengths, device="cuda", dtype=torch.int32)
+    ws = torch.empty(ops.qwen35_batched_decode_workspace_bytes(B, max_ctx, per * 2), device="cuda",
+                     dtype=torch.uint8)
+    out = torch.empty(B, HQ, D, device="cuda", dtype=torch.bfloat16)
+    ops.qwen35_online_attention_decode_batched(q, k, v, g, out, cache, lens, ws, max_ctx, per * 2)
+    torch.cuda.synchronize()
+    got = from_dev(out)
+    for b in range(B):
+        L = int(lengths[b])
+        shape = S(1, HQ, HKV, D, max_ctx, L - 1)
+        plan = ops.qwen35_online_decode_plan(shape, ops.AUTO, max_ctx)
+        nbytes = ops.qwen35_online_decode_workspace_layout(shape, plan[0])[4]
+        ws1 = torch.empty(nbytes, device="cuda", dtype=torch.uint8) if nbytes else None
+        one = torch.empty(HQ * D, device="cuda", dtype=torch.bfloat16)
+        ops.qwen35_online_attention_decode(q[b].flatten(), k[b].flatten(), v[b].flatten(), g[b].flatten(),
+                                           one, cache[b * per:(b + 1) * per], ws1, shape, 3, 1, 1,
+                                           plan=plan)
+        torch.cuda.synchronize()
+        assert_bf16_close(got[b], from_dev(one).reshape(HQ, D), what=f"cfg4 seq {b} len {L} vs single")
+    order = np.argsort(lengths)
+    for b in {int(order[0]), int(order[-1]), int(order[len(order) // 3]), int(order[2 * len(order) // 3])}:
+        L = int(lengths[b])
+        c = from_dev(cache[b * per:(b + 1) * per]).reshape(2, HKV, max_ctx, D)[:, :, :L]
+        keys, vals = c[0].transpose(1, 0, 2), c[1].transpose(1, 0, 2)
+        expect = orc.attention_core(from_dev(q[b])[None], keys, vals, from_dev(g[b])[None], L - 1)[0]
+        assert_bf16_close(got[b], bf16(expect), what=f"cfg4 seq {b} len {L} vs oracle")
