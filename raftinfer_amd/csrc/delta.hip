@@ -631,8 +631,10 @@ __device__ __forceinline__ void invert_unit_lower_64(const float (*a)[kLdC], flo
                                                      float (*y)[36]) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 15, lk = lane >> 4;
+  // Waves 0-3 do the work (a workgroup may have more); every wave takes the
+  // barriers.
   // 1. Diagonal blocks; zero the blocks right of the diagonal.
-  {
+  if (wave < 4) {
     const int b = 16 * wave;
     for (int j = 16 * (wave + 1) + lane; j < kChunk; j += 64)
 #pragma unroll
@@ -676,8 +678,8 @@ __device__ __forceinline__ void invert_unit_lower_64(const float (*a)[kLdC], flo
   }
   __syncthreads();
   // 3. Lower-left 32 x 32 block = -T_BR A_BL T_TL; wave w -> tile (2 + w/2, w%2).
-  const int ti = 2 + (wave >> 1), tj = wave & 1;
-  {
+  const int ti = 2 + ((wave & 3) >> 1), tj = wave & 1;
+  if (wave < 4) {
     // T_TL is lower triangular and its upper right block is stored as 0, so
     // the full k range gives the same sums; the operands are read up front.
     float av[8], bv[8];
@@ -693,7 +695,7 @@ __device__ __forceinline__ void invert_unit_lower_64(const float (*a)[kLdC], flo
     for (int r = 0; r < 4; ++r) y[16 * (ti - 2) + 4 * lk + r][16 * tj + lr] = acc[r];
   }
   __syncthreads();
-  {
+  if (wave < 4) {
     // T_BR is lower triangular with its upper right block stored as 0.
     float av[8], bv[8];
 #pragma unroll
@@ -740,11 +742,11 @@ __device__ __forceinline__ void split2(float a, float b, std::uint32_t &h, std::
 
 // Writes a [rows][cols] fp32 LDS tile (row stride LD) to a record as split
 // bf16 [2][rows][cols], 8 elements (two 16-byte stores) per item.
-template <int LD>
+template <int LD, int NT = 256>
 __device__ __forceinline__ void write_split_rows(const float (*src)[LD], int rows, int cols,
                                                  bf16_bits *dst) {
   const int per_row = cols / 8;
-  for (int item = threadIdx.x; item < rows * per_row; item += 256) {
+  for (int item = threadIdx.x; item < rows * per_row; item += NT) {
     const int r = item / per_row, c = 8 * (item % per_row);
     u32x4 hi, lo;
 #pragma unroll
@@ -894,6 +896,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
 // are exact bf16 products with fp32 accumulation; the T-weighted sums
 // W = T diag(beta e^G) K and U = T diag(beta) V take the fp32 left factor as a
 // (hi, lo) split, two MFMAs per k-step.  The record holds Q and K^T unscaled.
+constexpr int kPrepThreads = 512; // bf16 chunk prep: 8 waves, two per SIMD
+
 struct PrepBShared {
   union {
     struct {
@@ -928,7 +932,7 @@ __device__ __forceinline__ floatx4 mfma_b(const bf16_bits *a, const bf16_bits *b
       __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(b)), c, 0, 0, 0);
 }
 
-__global__ __launch_bounds__(256) void chunk_prep_bf16_kernel(Src<bf16_bits> qs, Src<bf16_bits> ks,
+__global__ __launch_bounds__(kPrepThreads) void chunk_prep_bf16_kernel(Src<bf16_bits> qs, Src<bf16_bits> ks,
                                                               Src<bf16_bits> vs,
                                                               const float *__restrict__ beta,
                                                               const float *__restrict__ gdecay,
@@ -944,23 +948,23 @@ __global__ __launch_bounds__(256) void chunk_prep_bf16_kernel(Src<bf16_bits> qs,
   const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
   unsigned char *record = scratch.at(h, blockIdx.y);
 
-  // Q rows: RowBlock map.  K and V: item (tid + 256 r) -> token pair
-  // 2 (item % 32) + {0, 1}, dims 8 (item / 32) .. +7, so the transposed tiles
-  // are written straight from registers, one dword (two tokens) per store.
-  // Rows past L repeat row L-1.
-  RowBlock<bf16_bits> qb;
-  qb.load(L, [&](int i, int d) { return src_row(qs, t0 + i, kh, d); });
-  Chunk8<bf16_bits> kp[2][2], vp[2][2];
+  // Q rows: item (tid + 512 r) -> row item / 16, dims 8 (item % 16) .. +7.
+  // K and V: thread -> token pair 2 (tid % 32) + {0, 1}, dims 8 (tid / 32)
+  // .. +7, so the transposed tiles are written straight from registers, one
+  // dword (two tokens) per store.  Rows past L repeat row L-1.
+  u32x4 qv[2];
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
-    const int item = tid + 256 * r;
-    const int j0 = 2 * (item & 31), d = 8 * (item >> 5);
+    const int p = tid + kPrepThreads * r, i = p >> 4, d = 8 * (p & 15);
+    qv[r] = *reinterpret_cast<const u32x4 *>(src_row(qs, t0 + (i < L ? i : L - 1), kh, d));
+  }
+  Chunk8<bf16_bits> kp[2], vp[2];
+  const int j0 = 2 * (tid & 31), dkv = 8 * (tid >> 5);
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int j = j0 + e < L ? j0 + e : L - 1;
-      kp[r][e].w = *reinterpret_cast<const u32x4 *>(src_row(ks, t0 + j, kh, d));
-      vp[r][e].w = *reinterpret_cast<const u32x4 *>(src_row(vs, t0 + j, h, d));
-    }
+  for (int e = 0; e < 2; ++e) {
+    const int j = j0 + e < L ? j0 + e : L - 1;
+    kp[e].w = *reinterpret_cast<const u32x4 *>(src_row(ks, t0 + j, kh, dkv));
+    vp[e].w = *reinterpret_cast<const u32x4 *>(src_row(vs, t0 + j, h, dkv));
   }
   float bt = 0.f, gt = 0.f;
   if (tid < L) {
@@ -969,26 +973,20 @@ __global__ __launch_bounds__(256) void chunk_prep_bf16_kernel(Src<bf16_bits> qs,
   }
   bf16_bits *qrec = reinterpret_cast<bf16_bits *>(record + rec::kQ);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int p = tid + 256 * r;
-    const int i = p >> 4, d = 8 * (p & 15);
-    *reinterpret_cast<u32x4 *>(&sh.r1.qk.q[i][d]) = qb.c[r].w;
-    *reinterpret_cast<u32x4 *>(qrec + i * kChunkDim + d) = qb.c[r].w;
-  }
-#pragma unroll
   for (int r = 0; r < 2; ++r) {
-    const int item = tid + 256 * r;
-    const int j0 = 2 * (item & 31), d = 8 * (item >> 5);
-    *reinterpret_cast<u32x4 *>(&sh.r1.qk.k[j0][d]) = kp[r][0].w;
-    *reinterpret_cast<u32x4 *>(&sh.r1.qk.k[j0 + 1][d]) = kp[r][1].w;
+    const int p = tid + kPrepThreads * r, i = p >> 4, d = 8 * (p & 15);
+    *reinterpret_cast<u32x4 *>(&sh.r1.qk.q[i][d]) = qv[r];
+    *reinterpret_cast<u32x4 *>(qrec + i * kChunkDim + d) = qv[r];
+  }
+  *reinterpret_cast<u32x4 *>(&sh.r1.qk.k[j0][dkv]) = kp[0].w;
+  *reinterpret_cast<u32x4 *>(&sh.r1.qk.k[j0 + 1][dkv]) = kp[1].w;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int sh16 = 16 * (e & 1);
-      const std::uint32_t k0 = (kp[r][0].w[e >> 1] >> sh16) & 0xFFFFu, k1 = (kp[r][1].w[e >> 1] >> sh16) & 0xFFFFu;
-      const std::uint32_t v0 = (vp[r][0].w[e >> 1] >> sh16) & 0xFFFFu, v1 = (vp[r][1].w[e >> 1] >> sh16) & 0xFFFFu;
-      *reinterpret_cast<std::uint32_t *>(&sh.kt[d + e][j0]) = k0 | (k1 << 16);
-      *reinterpret_cast<std::uint32_t *>(&sh.vt[d + e][j0]) = v0 | (v1 << 16);
-    }
+  for (int e = 0; e < 8; ++e) {
+    const int sh16 = 16 * (e & 1);
+    const std::uint32_t k0 = (kp[0].w[e >> 1] >> sh16) & 0xFFFFu, k1 = (kp[1].w[e >> 1] >> sh16) & 0xFFFFu;
+    const std::uint32_t v0 = (vp[0].w[e >> 1] >> sh16) & 0xFFFFu, v1 = (vp[1].w[e >> 1] >> sh16) & 0xFFFFu;
+    *reinterpret_cast<std::uint32_t *>(&sh.kt[dkv + e][j0]) = k0 | (k1 << 16);
+    *reinterpret_cast<std::uint32_t *>(&sh.vt[dkv + e][j0]) = v0 | (v1 << 16);
   }
   if (tid < kChunk) {
     sh.beta[tid] = bt;
@@ -999,81 +997,86 @@ __global__ __launch_bounds__(256) void chunk_prep_bf16_kernel(Src<bf16_bits> qs,
   __syncthreads();
   {
     bf16_bits *kr = reinterpret_cast<bf16_bits *>(record + rec::kKt);
-    u32x4 kv[4];
+    u32x4 kv[2];
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      const int item = tid + 256 * n, d = item >> 3, j = 8 * (item & 7);
+    for (int n = 0; n < 2; ++n) {
+      const int item = tid + kPrepThreads * n, d = item >> 3, j = 8 * (item & 7);
       kv[n] = *reinterpret_cast<const u32x4 *>(&sh.kt[d][j]);
     }
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      const int item = tid + 256 * n, d = item >> 3, j = 8 * (item & 7);
+    for (int n = 0; n < 2; ++n) {
+      const int item = tid + kPrepThreads * n, d = item >> 3, j = 8 * (item & 7);
       *reinterpret_cast<u32x4 *>(kr + d * kChunk + j) = kv[n];
     }
   }
   // M = e^{G_i-G_j} (q_i . k_j) q_scale k_scale (j <= i), A = beta_i e^{G_i-G_j}
-  // (k_i . k_j) k_scale^2 (j < i); wave w = row tile w, exact bf16 products.
+  // (k_i . k_j) k_scale^2 (j < i), exact bf16 products.  Wave w takes row
+  // tile ti = w % 4 and column tiles tj = 2 (w / 4) + {0, 1}; tiles above the
+  // diagonal are written as 0 without products.
   const float qk_scale = qs.scale * ks.scale, kk_scale = ks.scale * ks.scale;
-  // Per-lane decay and beta values, read once: rows i = 16 wave + 4 lk + r,
-  // columns j = 16 tj + lr.
-  float gi[4], bi[4], gj[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    gi[r] = sh.g[wave * 16 + lk * 4 + r];
-    bi[r] = sh.beta[wave * 16 + lk * 4 + r] * kk_scale;
-    gj[r] = sh.g[r * 16 + lr];
-  }
-  // Row operands (this wave's Q and K rows) are read once; each column tile's
-  // K rows are read before its eight products, and every product runs before
-  // any result is scaled, so LDS latency is paid about once per tile.
-  bf16x8 qrow[4], krow[4];
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    qrow[kk] = lds8(&sh.r1.qk.q[wave * 16 + lr][32 * kk + 8 * lk]);
-    krow[kk] = lds8(&sh.r1.qk.k[wave * 16 + lr][32 * kk + 8 * lk]);
-  }
-  floatx4 am[4], aa[4];
-#pragma unroll
-  for (int tj = 0; tj < 4; ++tj) {
-    am[tj] = floatx4{};
-    aa[tj] = floatx4{};
-    if (tj <= wave) {
-      bf16x8 kcol[4];
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) kcol[kk] = lds8(&sh.r1.qk.k[tj * 16 + lr][32 * kk + 8 * lk]);
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        am[tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qrow[kk], kcol[kk], am[tj], 0, 0, 0);
-        aa[tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(krow[kk], kcol[kk], aa[tj], 0, 0, 0);
-      }
-    }
-  }
-#pragma unroll
-  for (int tj = 0; tj < 4; ++tj) {
+  {
+    const int ti = wave & 3, tj0 = 2 * (wave >> 2);
+    // Per-lane decay and beta values, read once: rows i = 16 ti + 4 lk + r,
+    // columns j = 16 tj + lr.
+    float gi[4], bi[4], gj[2];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int i = wave * 16 + lk * 4 + r, j = tj * 16 + lr;
-      const float e = __expf(gi[r] - gj[tj]);
-      sh.mm[i][j] = (j <= i && i < L) ? am[tj][r] * qk_scale * e : 0.f;
-      sh.r3.at.a[i][j] = (j < i && i < L) ? bi[r] * e * aa[tj][r] : 0.f;
+      gi[r] = sh.g[ti * 16 + lk * 4 + r];
+      bi[r] = sh.beta[ti * 16 + lk * 4 + r] * kk_scale;
+    }
+#pragma unroll
+    for (int n = 0; n < 2; ++n) gj[n] = sh.g[(tj0 + n) * 16 + lr];
+    // Operands are read before the products, and every product runs before
+    // any result is scaled, so LDS latency is paid about once.
+    bf16x8 qrow[4], krow[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      qrow[kk] = lds8(&sh.r1.qk.q[ti * 16 + lr][32 * kk + 8 * lk]);
+      krow[kk] = lds8(&sh.r1.qk.k[ti * 16 + lr][32 * kk + 8 * lk]);
+    }
+    floatx4 am[2], aa[2];
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      am[n] = floatx4{};
+      aa[n] = floatx4{};
+      if (tj0 + n <= ti) {
+        bf16x8 kcol[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) kcol[kk] = lds8(&sh.r1.qk.k[(tj0 + n) * 16 + lr][32 * kk + 8 * lk]);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          am[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qrow[kk], kcol[kk], am[n], 0, 0, 0);
+          aa[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(krow[kk], kcol[kk], aa[n], 0, 0, 0);
+        }
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = ti * 16 + lk * 4 + r, j = (tj0 + n) * 16 + lr;
+        const float e = __expf(gi[r] - gj[n]);
+        sh.mm[i][j] = (j <= i && i < L) ? am[n][r] * qk_scale * e : 0.f;
+        sh.r3.at.a[i][j] = (j < i && i < L) ? bi[r] * e * aa[n][r] : 0.f;
+      }
     }
   }
   __syncthreads();
   invert_unit_lower_64(sh.r3.at.a, sh.r3.at.tm, sh.r1.y);
   // tw = T diag(beta e^G k_scale), tu = T diag(beta v_scale), split.
-  // Thread -> column pair j = 2 (tid % 32), rows tid / 32 + 8 n: the column
-  // factors are read once and the eight row pairs in one batch.
+  // Thread -> column pair j = 2 (tid % 32), rows tid / 32 + 16 n: the column
+  // factors are read once and the four row pairs in one batch.
   {
     const int j = 2 * (tid & 31), i0 = tid >> 5;
     const float b0 = sh.beta[j], b1 = sh.beta[j + 1];
     const float fw0 = b0 * __expf(sh.g[j]) * ks.scale, fw1 = b1 * __expf(sh.g[j + 1]) * ks.scale;
     const float fu0 = b0 * vs.scale, fu1 = b1 * vs.scale;
-    float2 tv[8];
+    float2 tv[4];
 #pragma unroll
-    for (int n = 0; n < 8; ++n) tv[n] = *reinterpret_cast<const float2 *>(&sh.r3.at.tm[i0 + 8 * n][j]);
+    for (int n = 0; n < 4; ++n) tv[n] = *reinterpret_cast<const float2 *>(&sh.r3.at.tm[i0 + 16 * n][j]);
 #pragma unroll
-    for (int n = 0; n < 8; ++n) {
-      const int i = i0 + 8 * n;
+    for (int n = 0; n < 4; ++n) {
+      const int i = i0 + 16 * n;
       std::uint32_t hi, lo;
       split2(tv[n].x * fw0, tv[n].y * fw1, hi, lo);
       *reinterpret_cast<std::uint32_t *>(&sh.tw[0][i][j]) = hi;
@@ -1084,11 +1087,11 @@ __global__ __launch_bounds__(256) void chunk_prep_bf16_kernel(Src<bf16_bits> qs,
     }
   }
   __syncthreads();
-  // W = tw K, U = tu V (B operands K^T, V^T): 4 x 8 tiles, wave w takes w + 4n.
-  floatx4 aw[8], au[8];
+  // W = tw K, U = tu V (B operands K^T, V^T): 4 x 8 tiles, wave w takes w + 8n.
+  floatx4 aw[4], au[4];
 #pragma unroll
-  for (int n = 0; n < 8; ++n) {
-    const int tile = wave + 4 * n;
+  for (int n = 0; n < 4; ++n) {
+    const int tile = wave + 8 * n;
     const int ti = tile >> 3, tn = tile & 7;
     aw[n] = floatx4{};
     au[n] = floatx4{};
@@ -1103,8 +1106,8 @@ __global__ __launch_bounds__(256) void chunk_prep_bf16_kernel(Src<bf16_bits> qs,
   }
   __syncthreads(); // q/k and a/tm no longer needed: stage W and U
 #pragma unroll
-  for (int n = 0; n < 8; ++n) {
-    const int tile = wave + 4 * n;
+  for (int n = 0; n < 4; ++n) {
+    const int tile = wave + 8 * n;
     const int ti = tile >> 3, tn = tile & 7;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -1113,11 +1116,11 @@ __global__ __launch_bounds__(256) void chunk_prep_bf16_kernel(Src<bf16_bits> qs,
     }
   }
   __syncthreads();
-  write_split_rows<kLd>(sh.r1.w, kChunk, kChunkDim, reinterpret_cast<bf16_bits *>(record + rec::kW));
-  write_split_rows<kLdC>(sh.mm, kChunk, kChunk, reinterpret_cast<bf16_bits *>(record + rec::kM));
+  write_split_rows<kLd, kPrepThreads>(sh.r1.w, kChunk, kChunkDim, reinterpret_cast<bf16_bits *>(record + rec::kW));
+  write_split_rows<kLdC, kPrepThreads>(sh.mm, kChunk, kChunk, reinterpret_cast<bf16_bits *>(record + rec::kM));
   {
     float *u = reinterpret_cast<float *>(record + rec::kU);
-    for (int item = tid; item < kChunk * (kChunkDim / 4); item += 256) {
+    for (int item = tid; item < kChunk * (kChunkDim / 4); item += kPrepThreads) {
       const int r = item / (kChunkDim / 4), c = 4 * (item % (kChunkDim / 4));
       *reinterpret_cast<float4 *>(u + r * kChunkDim + c) =
           make_float4(sh.r3.u[r][c], sh.r3.u[r][c + 1], sh.r3.u[r][c + 2], sh.r3.u[r][c + 3]);
@@ -1460,7 +1463,7 @@ void launch_recurrence(Src<InT> q, Src<InT> k, Src<InT> v, const float *beta, co
   if (chunked) {
     const dim3 pgrid{static_cast<unsigned>(hv), static_cast<unsigned>(ceil_div_unchecked(tokens, kChunk)), 1};
     if constexpr (std::is_same_v<InT, bf16_bits>)
-      chunk_prep_bf16_kernel<<<pgrid, 256, 0, stream>>>(q, k, v, beta, g, scratch, tokens, hk, hv);
+      chunk_prep_bf16_kernel<<<pgrid, kPrepThreads, 0, stream>>>(q, k, v, beta, g, scratch, tokens, hk, hv);
     else
       chunk_prep_kernel<InT><<<pgrid, 256, 0, stream>>>(q, k, v, beta, g, scratch, tokens, hk, hv);
     check_launch<Err>("qwen35_gated_delta chunk preparation");
