@@ -1087,32 +1087,46 @@ __global__ __launch_bounds__(kPrepThreads) void chunk_prep_bf16_kernel(Src<bf16_
     }
   }
   __syncthreads();
-  // W = tw K, U = tu V (B operands K^T, V^T): 4 x 8 tiles, wave w takes w + 8n.
+  // W = tw K, U = tu V (B operands K^T, V^T): 4 x 8 tiles (ti, tn); wave w
+  // takes tn = w and ti = 0..3, so its K^T and V^T operands are read once and
+  // each row tile's operands before its eight products.
   floatx4 aw[4], au[4];
+  {
+    bf16x8 kc[2], vc[2];
 #pragma unroll
-  for (int n = 0; n < 4; ++n) {
-    const int tile = wave + 8 * n;
-    const int ti = tile >> 3, tn = tile & 7;
-    aw[n] = floatx4{};
-    au[n] = floatx4{};
+    for (int jj = 0; jj < 2; ++jj) {
+      kc[jj] = lds8(&sh.kt[wave * 16 + lr][32 * jj + 8 * lk]);
+      vc[jj] = lds8(&sh.vt[wave * 16 + lr][32 * jj + 8 * lk]);
+    }
 #pragma unroll
-    for (int jj = 0; jj < kChunk; jj += 32) {
-      const int ja = jj + 8 * lk;
-      aw[n] = mfma_b(&sh.tw[0][ti * 16 + lr][ja], &sh.kt[tn * 16 + lr][ja], aw[n]);
-      aw[n] = mfma_b(&sh.tw[1][ti * 16 + lr][ja], &sh.kt[tn * 16 + lr][ja], aw[n]);
-      au[n] = mfma_b(&sh.tu[0][ti * 16 + lr][ja], &sh.vt[tn * 16 + lr][ja], au[n]);
-      au[n] = mfma_b(&sh.tu[1][ti * 16 + lr][ja], &sh.vt[tn * 16 + lr][ja], au[n]);
+    for (int ti = 0; ti < 4; ++ti) {
+      bf16x8 w0[2], w1[2], u0[2], u1[2];
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int ja = 32 * jj + 8 * lk;
+        w0[jj] = lds8(&sh.tw[0][ti * 16 + lr][ja]);
+        w1[jj] = lds8(&sh.tw[1][ti * 16 + lr][ja]);
+        u0[jj] = lds8(&sh.tu[0][ti * 16 + lr][ja]);
+        u1[jj] = lds8(&sh.tu[1][ti * 16 + lr][ja]);
+      }
+      aw[ti] = floatx4{};
+      au[ti] = floatx4{};
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        aw[ti] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0[jj], kc[jj], aw[ti], 0, 0, 0);
+        au[ti] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(u0[jj], vc[jj], au[ti], 0, 0, 0);
+        aw[ti] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1[jj], kc[jj], aw[ti], 0, 0, 0);
+        au[ti] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(u1[jj], vc[jj], au[ti], 0, 0, 0);
+      }
     }
   }
   __syncthreads(); // q/k and a/tm no longer needed: stage W and U
 #pragma unroll
-  for (int n = 0; n < 4; ++n) {
-    const int tile = wave + 8 * n;
-    const int ti = tile >> 3, tn = tile & 7;
+  for (int ti = 0; ti < 4; ++ti) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      sh.r1.w[ti * 16 + lk * 4 + r][tn * 16 + lr] = aw[n][r];
-      sh.r3.u[ti * 16 + lk * 4 + r][tn * 16 + lr] = au[n][r];
+      sh.r1.w[ti * 16 + lk * 4 + r][wave * 16 + lr] = aw[ti][r];
+      sh.r3.u[ti * 16 + lk * 4 + r][wave * 16 + lr] = au[ti][r];
     }
   }
   __syncthreads();
