@@ -260,6 +260,52 @@ def test_prefill_adversarial_rescaling(gpu, act, cdt):
     assert close_enough(out, expect)
 
 
+@pytest.mark.parametrize("direction", [1, -1])
+@pytest.mark.parametrize("past", [0, 64])
+def test_prefill_mfma_adversarial_rescaling_model_shape(gpu, direction, past):
+    # The -80 .. +80 score ramp of cpp/tests/qwen35_cuda_attention_test.cu:709-750 at the
+    # model shape, so the bf16 MFMA kernel runs.  Ascending, every 32-key tile raises the
+    # running max by ~14 log2 units (a rescale each tile, past the lazy threshold); descending,
+    # the first keys dominate and later tiles underflow.  past > 0 reads keys from the cache.
+    T = 512
+    n = past + T
+    ramp = (-80.0 + 160.0 * np.arange(n) / (n - 1)) * direction
+    q = np.zeros((T, HQ, D), np.float32)
+    q[:, :, 0] = 16.0  # score = q.k / 16 = k[0]
+    kall = np.zeros((n, HKV, D), np.float32)
+    kall[:, :, 0] = ramp[:, None]
+    vall = np.zeros((n, HKV, D), np.float32)
+    for h in range(HKV):
+        vall[:, h] = 0.01 * (np.arange(n)[:, None] % 97 + np.arange(D)[None, :] + h)
+    g = normal(rng(5), T, HQ, D)
+    out, expect, *_ = run_prefill(3, 1, 1, T, HQ, HKV, D, past,
+                                  inputs=(q, g, kall[past:], vall[past:], kall[:past], vall[:past]))
+    assert np.isfinite(out).all()
+    assert_bf16_close(out, bf16(expect), what=f"adversarial ramp dir {direction} past {past}")
+
+
+def test_prefill_mfma_pp2048_vs_torch_fp32(gpu):
+    # PP2048 (the size bench.py also times) against a torch fp32 causal attention on the
+    # same bf16 inputs: the C oracle takes minutes at this size.  Same bf16 gates.
+    T = 2048
+    gen = torch.Generator(device="cuda").manual_seed(2048)
+    rnd = lambda *shape: torch.randn(*shape, device="cuda", generator=gen).to(torch.bfloat16)
+    q, g, k, v = rnd(T, HQ, D), rnd(T, HQ, D), rnd(T, HKV, D), rnd(T, HKV, D)
+    cache = torch.zeros(2 * T * HKV * D, device="cuda", dtype=torch.bfloat16)
+    out = torch.empty(T, HQ, D, device="cuda", dtype=torch.bfloat16)
+    shape = S(T, HQ, HKV, D, T, 0)
+    ops.qwen35_causal_attention(q, k, v, g, out, cache, None, shape, 3,
+                                ops.Qwen35AttentionLaunchPolicy(1, 1, 1))
+    torch.cuda.synchronize()
+    qf = q.float().permute(1, 0, 2)                                # [16][T][256]
+    kf = k.float().repeat_interleave(HQ // HKV, dim=1).permute(1, 0, 2)
+    vf = v.float().repeat_interleave(HQ // HKV, dim=1).permute(1, 0, 2)
+    s = torch.matmul(qf, kf.transpose(1, 2)) / 16.0
+    s = s.masked_fill(torch.triu(torch.ones(T, T, device="cuda", dtype=torch.bool), 1), float("-inf"))
+    ref = torch.matmul(torch.softmax(s, dim=-1), vf).permute(1, 0, 2) * torch.sigmoid(g.float())
+    assert_bf16_close(from_dev(out), bf16(from_dev(ref)), what="PP2048 vs torch fp32")
+
+
 @pytest.mark.parametrize("act", [1, 2, 3])
 @pytest.mark.parametrize("T,past", [(17, 0), (1, 40), (5, 7)])
 def test_materialized_path(gpu, act, T, past):
