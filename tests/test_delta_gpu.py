@@ -136,6 +136,23 @@ def test_model_shape_schedules(gpu, T, schedule):
     assert rel_l2(got[2], want[2]) < 1e-4
 
 
+@pytest.mark.parametrize("dt,wdt", [(1, 1), (2, 2), (1, 3)])
+def test_model_shape_chunked_f32_f16_activations(gpu, dt, wdt):
+    # The chunked path (T >= 64, two chunks with a ragged tail) with f32 / f16 activations and
+    # f32 or bf16 auxiliary weights: these go through the f32 chunk prep and the hi/lo
+    # (inexact) scan.
+    T = 100
+    sh = model_shape(T)
+    fx = fixture_for(sh, seed=T + dt)
+    r = rng(T + 7)
+    rec0 = normal(r, 32 * 128 * 128, scale=0.05)
+    conv0 = normal(r, 8192 * 3)
+    got = run_gpu(sh, fx, dt, wdt, conv0, rec0)
+    want = run_ref(sh, fx, dt, wdt, conv0, rec0)
+    check(got, want)
+    assert rel_l2(got[2], want[2]) < 1e-4
+
+
 def cfg5_inputs(T, seed):
     """q, k ~ N(0,1) L2-normalised per head, v ~ N(0,1),
     beta = sigmoid(N), g = -softplus(N); bf16 q/k/v."""
