@@ -1,11 +1,11 @@
 """Benchmark of the gfx950 attention / gated-delta hot path.
 
-A "step" is one split-K GQA decode call at context 4096 (
+A "step" is one split-K GQA decode call at context 4096 (benchmark config 2:
 16 query / 4 KV heads, head_dim 256, BF16 head-major cache, 256-token
 partitions + fp32 LSE merge), with inputs resident in HBM and 40 distinct
 caches (671 MB) rotated so the 256 MB MALL cannot serve them.  ``value`` is
 that call's algorithmic HBM throughput (KV bytes + q/gate/out bytes per call /
-event-timed call time).  The other BASELINE configs are reported under
+event-timed call time).  The other benchmark configs are reported under
 ``configs``; ``roofline`` prices the dominant kernel (the split-K partition
 kernel) timed alone with HIP events on its own stream; ``cpu_baseline`` times
 the CPU oracle's decode on one host core over a bounded sample.
@@ -60,7 +60,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(sharding is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+              "(the path would shard over KV heads and value heads); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

@@ -3,7 +3,7 @@
 Mirrors the reference's cpp/tests/qwen35_cuda_attention_test.cu cases
 (decode in every layout / dtype, split-K boundary contexts with partial-state
 checks, the capacity guard, online prefill incl. causality and adversarial
-rescaling, the materialized path) plus the BASELINE shapes.  Gates:
+rescaling, the materialized path) plus the benchmark shapes.  Gates:
  * bf16 outputs: max-abs 1e-2 (or one bf16 ulp of the expected value) and
    relative-L2 5e-3 against the fp32-accumulated oracle;
  * reference-style cases: abs <= 2e-2 or rel <= 2e-2 elementwise;
@@ -72,7 +72,7 @@ def run_decode(act, cdt, layout, ctx, max_ctx, mode=None, device_position=True, 
 
 
 def test_decode_cfg1_single_block_ctx512(gpu):
-    # ctx 512, bf16 head-major cache, single-block, no split.
+    # benchmark config 1: ctx 512, bf16 head-major cache, single-block, no split.
     out, expect, cache, keys, vals, _, _ = run_decode(3, 1, 1, 512, 512, mode=None,
                                                       device_position=False, seed=11)
     assert_bf16_close(out, bf16(expect), what="cfg1 decode")
@@ -139,7 +139,7 @@ def test_split_k_512(gpu, ctx):
 
 @pytest.mark.parametrize("ctx", [4096, 16384])
 def test_split_k_cfg2_long_context(gpu, ctx):
-    # auto (split-K 256), ~1% of K rows x8, host position.
+    # benchmark config 2: auto (split-K 256), ~1% of K rows x8, host position.
     out, expect, *_ = run_decode(3, 1, 1, ctx, ctx, mode=0, device_position=False, seed=ctx,
                                  heavy_rows=0.01)
     assert_bf16_close(out, bf16(expect), what=f"cfg2 ctx {ctx}")
@@ -208,7 +208,7 @@ def run_prefill(act, cdt, layout, T, hq, hkv, d, past, seed=0, inputs=None):
 @pytest.mark.parametrize("T", [17, 128, 512])
 @pytest.mark.parametrize("past", [0, 111])
 def test_prefill_mfma_model_shape(gpu, T, past):
-    # BASELINE config 3 (PP128 / PP512) and the reference's {17,16,4,256,111} case.
+    # benchmark config 3 (PP128 / PP512) and the reference's {17,16,4,256,111} case.
     out, expect, cache, keys, vals = run_prefill(3, 1, 1, T, HQ, HKV, D, past, seed=T + past)
     assert_bf16_close(out, bf16(expect), what=f"prefill T={T} past={past}")
     ck, cv = read_cache(cache, 1, past + T, past + T)
@@ -339,7 +339,7 @@ def test_materialized_path(gpu, act, T, past):
     ([16641, 700], 16896),
 ])
 def test_batched_ragged_decode(gpu, lengths, max_ctx):
-    # BASELINE config 4 at reduced length: per-sequence oracle, mixed policies.
+    # benchmark config 4 at reduced length: per-sequence oracle, mixed policies.
     B = len(lengths)
     r = rng(77)
     per = 2 * max_ctx * HKV * D
@@ -369,7 +369,7 @@ def test_batched_ragged_decode(gpu, lengths, max_ctx):
 
 
 def test_batched_ragged_decode_cfg4_full_size(gpu):
-    # BASELINE config 4 at full size: 32 sequences with lengths U{1..32768} from the bench's
+    # benchmark config 4 at full size: 32 sequences with lengths U{1..32768} from the bench's
     # seed, max_ctx 32768, bf16 head-major caches (4.3 GB).  Every sequence is checked against
     # the single-sequence decode entry point (pinned to the oracle by the tests above) on the
     # same, already appended cache; the shortest, the longest and two others also against the

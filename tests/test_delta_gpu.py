@@ -2,7 +2,7 @@
 
 Mirrors cpp/tests/qwen35_cuda_delta_test.cu (prefill lengths, continued
 prefill, decode after prefill, f32 auxiliary weights, f32 activations, the
-model-shape register path, both schedules) and BASELINE config 5 (chunked
+model-shape register path, both schedules) and benchmark config 5 (chunked
 prefill T=512 in chunks of 64, then 32 recurrent decode steps).  Operands are
 quantised to the activation dtype before the fp32 oracle runs
 (cpp/tests/qwen35_cuda_delta_test.cu:258-276).  Gates: the reference's
@@ -154,7 +154,7 @@ def test_model_shape_chunked_f32_f16_activations(gpu, dt, wdt):
 
 
 def cfg5_inputs(T, seed):
-    """q, k ~ N(0,1) L2-normalised per head, v ~ N(0,1),
+    """benchmark config 5: q, k ~ N(0,1) L2-normalised per head, v ~ N(0,1),
     beta = sigmoid(N), g = -softplus(N); bf16 q/k/v."""
     r = rng(seed)
     q, k = normal(r, T, 16, 128), normal(r, T, 16, 128)
