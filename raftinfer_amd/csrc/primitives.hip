@@ -110,17 +110,16 @@ template <> struct Vec4<_Float16> {
 // lane l owns dims 4l .. 4l+3 of a head vector (whole-row loads and stores);
 // the rotation partner of dims 4l.. sits in lane l +- rotary_dim/8 and comes
 // over the lane crossbar.  Rotation angles: inv_freq_p = r^p with
-// r = base^(-2/rotary_dim) (one double pow per workgroup, then double
-// products), theta = position * inv_freq_p reduced modulo 2 pi in double,
-// then a float sincos of the reduced angle.
+// r = base^(-2/rotary_dim) (one double pow on the host, passed in; double
+// products here), theta = position * inv_freq_p reduced modulo 2 pi in
+// double, then a float sincos of the reduced angle.
 template <typename T, typename Wt>
 __global__ __launch_bounds__(kNormThreads) void norm_rope_256_kernel(
     const T *__restrict__ input, const Wt *__restrict__ weight, T *__restrict__ output,
     T *__restrict__ gate, std::size_t heads, std::size_t in_stride, std::size_t rotary_dim,
-    std::size_t position_offset, float rope_base, float epsilon,
+    std::size_t position_offset, double ratio, float epsilon,
     const std::uint32_t *device_position) {
   __shared__ float rot[256]; // [pairs] cos, then [pairs] sin (pairs <= 128)
-  __shared__ double ratio;
   constexpr int kWaves = kNormThreads / 64, kBatch = 4;
   const std::size_t token = blockIdx.x;
   const int pairs = static_cast<int>(rotary_dim / 2);
@@ -141,8 +140,6 @@ __global__ __launch_bounds__(kNormThreads) void norm_rope_256_kernel(
   };
   if (static_cast<std::size_t>(wave) < heads) load_batch(wave);
   Vec4<Wt>::load(weight + d0, w);
-  if (threadIdx.x == 0) ratio = pow(static_cast<double>(rope_base), -2.0 / static_cast<double>(rotary_dim));
-  __syncthreads();
   if (static_cast<int>(threadIdx.x) < pairs) {
     const int p = threadIdx.x;
     double inv = 1.0, bsq = ratio;
@@ -285,8 +282,9 @@ void launch_norm_rope(const void *input, const void *weight, void *output, void 
       aligned(output, vec_bytes) && aligned(gate, vec_bytes) && aligned(weight, wvec_bytes)) {
     norm_rope_256_kernel<T, Wt><<<static_cast<unsigned>(s.tokens), kNormThreads, 0, stream>>>(
         static_cast<const T *>(input), static_cast<const Wt *>(weight), static_cast<T *>(output),
-        static_cast<T *>(gate), s.heads, in_stride, s.rotary_dim, s.position_offset, s.rope_base,
-        epsilon, device_position);
+        static_cast<T *>(gate), s.heads, in_stride, s.rotary_dim, s.position_offset,
+        std::pow(static_cast<double>(s.rope_base), -2.0 / static_cast<double>(s.rotary_dim)), epsilon,
+        device_position);
     return;
   }
   const std::size_t lds = (s.rotary_dim / 2) * 2 * sizeof(float);
