@@ -154,6 +154,7 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
   const std::size_t col_head = kv_head * kGroup + (col >> 3);
   const int wave_u = __builtin_amdgcn_readfirstlane(wave); // wave index as a scalar
   WaveTile &tile = sh.tile[wave_u];
+  constexpr int kLateLoads = 4 + (FromInput ? 2 : 0); // gate (+ append) loads per thread
 
   floatx16 o[8];
 #pragma unroll
@@ -207,32 +208,6 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
       v_base[j] = chunk_offset(trow, d >> 3) + (d & 7);
     }
   }
-  // Append (FromInput): thread -> two 16-byte pieces of this workgroup's K/V
-  // rows (2 planes x 8 tokens x 32 pieces); loaded now, stored at the end.
-  u32x4 app[2];
-  if constexpr (FromInput) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int idx = tid + kThreads * j; // 0 .. 511
-      const int pl = idx >> 8, tok = (idx >> 5) & 7, piece = idx & 31;
-      const std::size_t tt = static_cast<std::size_t>(tok) < q_rows ? tok : q_rows - 1;
-      const bf16_bits *src = (pl ? value_in : key_in) + ((t0 + tt) * kKvHeads + kv_head) * kHeadDim;
-      app[j] = *reinterpret_cast<const u32x4 *>(src + 8 * piece);
-    }
-  }
-  // Gate rows of this workgroup, loaded first and held in registers until the
-  // epilogue: token tt's four heads are 2 KiB contiguous, read in 16-byte
-  // pieces (thread -> pieces tid + 256 j: token idx >> 7, piece idx & 127), so
-  // each load instruction covers whole 128-byte lines.
-  const std::size_t io_base = (t0 * kQueryHeads + kv_head * kGroup) * kHeadDim;
-  u32x4 gc[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int idx = tid + kThreads * j, tt = idx >> 7, piece = idx & 127;
-    gc[j] = u32x4{0u, 0u, 0u, 0u};
-    if (static_cast<std::size_t>(tt) < q_rows)
-      gc[j] = *reinterpret_cast<const u32x4 *>(gate + io_base + tt * kQueryHeads * kHeadDim + 8 * piece);
-  }
   // Q tile -> LDS, row = column c (token c % 8 of head 4 kv + c / 8), in the
   // K tile's chunk order; wave w loads rows 8w .. 8w+7 (4 instructions).
   {
@@ -249,20 +224,50 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
     }
   }
   std::size_t t = wave_u;
-  // Issue order: K(t0) V(t0) | K(t+4) V(t+4) per tile t, so 16 loads follow
-  // K(t) when it is waited for, and 16 (or none on the last tile) follow V(t).
+  // Issue order: Q, K(t0), V(t0), then the append and gate loads (kLateLoads,
+  // needed only at the end) | K(t+4) V(t+4) per tile t, so 16 loads (plus
+  // kLateLoads on the first tile) follow K(t) when it is waited for, and 16
+  // (or none on the last tile, plus kLateLoads on the first) follow V(t).
   if (t < n_tiles) {
     issue(k_src, lds_k, t * kKTile);
     issue(v_src, lds_v, t * kKTile);
   }
+  // Append (FromInput): thread -> two 16-byte pieces of this workgroup's K/V
+  // rows (2 planes x 8 tokens x 32 pieces); loaded now, stored at the end.
+  u32x4 app[2];
+  if constexpr (FromInput) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int idx = tid + kThreads * j; // 0 .. 511
+      const int pl = idx >> 8, tok = (idx >> 5) & 7, piece = idx & 31;
+      const std::size_t tt = static_cast<std::size_t>(tok) < q_rows ? tok : q_rows - 1;
+      const bf16_bits *src = (pl ? value_in : key_in) + ((t0 + tt) * kKvHeads + kv_head) * kHeadDim;
+      app[j] = *reinterpret_cast<const u32x4 *>(src + 8 * piece);
+    }
+  }
+  // Gate rows of this workgroup, held in registers until the epilogue: token
+  // tt's four heads are 2 KiB contiguous, read in 16-byte pieces (thread ->
+  // pieces tid + 256 j: token idx >> 7, piece idx & 127), so each load
+  // instruction covers whole 128-byte lines.  Rows past q_rows read row
+  // q_rows - 1 (never stored), so every thread issues exactly kLateLoads
+  // loads here, which the waits below count.
+  const std::size_t io_base = (t0 * kQueryHeads + kv_head * kGroup) * kHeadDim;
+  u32x4 gc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int idx = tid + kThreads * j, tt = idx >> 7, piece = idx & 127;
+    const std::size_t tr = static_cast<std::size_t>(tt) < q_rows ? tt : q_rows - 1;
+    gc[j] = *reinterpret_cast<const u32x4 *>(gate + io_base + tr * kQueryHeads * kHeadDim + 8 * piece);
+  }
 
-  if (t < n_tiles) wait_vm<32>(); else wait_vm<0>(); // this wave's Q rows have landed
+  if (t < n_tiles) wait_vm<32 + kLateLoads>(); else wait_vm<0>(); // this wave's Q rows have landed
   __syncthreads(); // ... and every other wave's
   for (; t < n_tiles; t += kWaves) {
     const std::size_t k0 = t * kKTile;
     const bool more = t + kWaves < n_tiles;
     const std::size_t k0_next = k0 + kWaves * kKTile;
-    wait_vm<16>(); // K(t) has landed; V(t) may still be in flight
+    const bool first = t == static_cast<std::size_t>(wave_u);
+    if (first) wait_vm<16 + kLateLoads>(); else wait_vm<16>(); // K(t) has landed; V(t) may still be in flight
     // S^T = K Q^T: A row = key `col` of the tile (lane & 31), k-half `half`.
     // Chunk 2 kb + half of row `col` sits at (2 (kb & 3) + half) ^ (col & 7)
     // + 8 (kb >> 2): four lane bases plus constant offsets.
@@ -327,7 +332,11 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
                                                 pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])});
     }
 
-    if (more) wait_vm<16>(); else wait_vm<0>(); // V(t) has landed
+    if (first) {
+      if (more) wait_vm<16 + kLateLoads>(); else wait_vm<kLateLoads>(); // V(t) has landed
+    } else {
+      if (more) wait_vm<16>(); else wait_vm<0>();
+    }
     // O^T += V^T P^T.  k-slot (kb, half, j) <-> key 16 kb + 4 half + j (j < 4)
     // and 16 kb + 8 + 4 half + (j - 4) (j >= 4), the P^T register order.  A
     // row (dim) 32 nb + 16 (g & 1) + r of 16-lane group g: source lane r of
