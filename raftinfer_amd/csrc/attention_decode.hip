@@ -306,17 +306,31 @@ __global__ __launch_bounds__(WAVES * 64) void decode_single_mfma_kernel(
   int dq;
   xcd_unit<DS>(blockIdx.x, kv_head, dq);
   if (kv_head >= kKvHeads) return;
+  // The gate values of this thread's outputs are loaded before the scan, so
+  // the epilogue does not wait for a load round trip of its own.
+  constexpr int kOut = (kGroup * DIMS + WAVES * 64 - 1) / (WAVES * 64);
+  float gv[kOut];
+#pragma unroll
+  for (int n = 0; n < kOut; ++n) {
+    const int o = threadIdx.x + n * WAVES * 64;
+    gv[n] = 0.f;
+    if (o < kGroup * DIMS)
+      gv[n] = bf16_to_f32(gate[(kv_head * kGroup + o / DIMS) * kHeadDim + dq * DIMS + o % DIMS]);
+  }
   decode_mfma_scan<DS, WAVES>(a, kv_head, dq, 0, ctx, position, sh);
   __syncthreads();
   // The scan read the new row from key/value; the cache copy goes last so its
   // load latency is not on the critical path.
   if (dq == 0) append_rows(a, kv_head, position);
-  for (int o = threadIdx.x; o < kGroup * DIMS; o += WAVES * 64) {
+#pragma unroll
+  for (int n = 0; n < kOut; ++n) {
+    const int o = threadIdx.x + n * WAVES * 64;
+    if (o >= kGroup * DIMS) break;
     const int h = o / DIMS, d = o % DIMS;
     float mm, l, acc;
     decode_mfma_combine(sh, h, d, mm, l, acc);
     const std::size_t idx = (kv_head * kGroup + h) * kHeadDim + dq * DIMS + d;
-    output[idx] = f32_to_bf16((acc / l) * sigmoid_gate(bf16_to_f32(gate[idx])));
+    output[idx] = f32_to_bf16((acc / l) * sigmoid_gate(gv[n]));
   }
 }
 
@@ -804,17 +818,32 @@ __global__ __launch_bounds__(WAVES * 64) void batched_mfma_kernel(
   const DecodeMfmaArgs a{query + seq * kQueryHeads * kHeadDim, key + seq * kKvHeads * kHeadDim,
                          value + seq * kKvHeads * kHeadDim, cache, cache, max_ctx, true};
   const std::size_t pos = ctx - 1;
+  // Single-block sequences: the gate values of this thread's outputs are
+  // loaded before the scan (no load round trip in the epilogue).
+  constexpr int kOut = (kGroup * DIMS + WAVES * 64 - 1) / (WAVES * 64);
+  float gv[kOut];
+#pragma unroll
+  for (int n = 0; n < kOut; ++n) {
+    const int o = threadIdx.x + n * WAVES * 64;
+    gv[n] = 0.f;
+    if (single && o < kGroup * DIMS)
+      gv[n] = bf16_to_f32(gate[(seq * kQueryHeads + kv_head * kGroup + o / DIMS) * kHeadDim + dq * DIMS +
+                               o % DIMS]);
+  }
   decode_mfma_scan<DS, WAVES, CT>(a, kv_head, dq, begin, end, pos, sh);
   __syncthreads();
   if (dq == 0 && pos >= begin && pos < end) append_rows(a, kv_head, pos);
-  for (int o = threadIdx.x; o < kGroup * DIMS; o += WAVES * 64) {
+#pragma unroll
+  for (int n = 0; n < kOut; ++n) {
+    const int o = threadIdx.x + n * WAVES * 64;
+    if (o >= kGroup * DIMS) break;
     const int h = o / DIMS, d = o % DIMS;
     float mm, l, acc;
     decode_mfma_combine(sh, h, d, mm, l, acc);
     const std::size_t head = seq * kQueryHeads + kv_head * kGroup + h;
     if (single) {
       const std::size_t idx = head * kHeadDim + dq * DIMS + d;
-      output[idx] = f32_to_bf16((acc / l) * sigmoid_gate(bf16_to_f32(gate[idx])));
+      output[idx] = f32_to_bf16((acc / l) * sigmoid_gate(gv[n]));
     } else {
       const std::size_t idx = head * max_partitions + partition;
       if (dq == 0 && d == 0) {
