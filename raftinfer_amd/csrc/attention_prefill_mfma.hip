@@ -372,6 +372,18 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
   }
 
 
+  // Append (FromInput): every wave has waited for all of its loads by now, so
+  // the cache rows go out here and drain under the merge and the epilogue.
+  if constexpr (FromInput) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int idx = tid + kThreads * j;
+      const int pl = idx >> 8, tok = (idx >> 5) & 7, piece = idx & 31;
+      if (static_cast<std::size_t>(tok) < q_rows)
+        *reinterpret_cast<u32x4 *>(cache + pl * plane + cache_row(head_major, t0 + tok, kv_head, max_ctx) +
+                                   8 * piece) = app[j];
+    }
+  }
   __syncthreads(); // every wave is done with its tile (and with Q)
   // The gate goes to the Q area as [column][256] rows, 16-byte chunk k of row
   // c at k ^ (c & 31): the epilogue's 8-byte reads (32 rows, one chunk) then
@@ -457,16 +469,6 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
     if (static_cast<std::size_t>(tt) < q_rows)
       *reinterpret_cast<u32x4 *>(output + io_base + tt * kQueryHeads * kHeadDim + 8 * piece) =
           *reinterpret_cast<const u32x4 *>(sh.q + io_offset((piece >> 5) * kQTok + tt, piece & 31));
-  }
-  if constexpr (FromInput) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int idx = tid + kThreads * j;
-      const int pl = idx >> 8, tok = (idx >> 5) & 7, piece = idx & 31;
-      if (static_cast<std::size_t>(tok) < q_rows)
-        *reinterpret_cast<u32x4 *>(cache + pl * plane + cache_row(head_major, t0 + tok, kv_head, max_ctx) +
-                                   8 * piece) = app[j];
-    }
   }
 }
 
