@@ -29,10 +29,11 @@
 //               of one dim), eight MFMAs' operands at a time.  The O^T
 //               accumulators stay in AGPRs (inline-asm MFMA).
 // The waves' partial (max, sum, O) are merged through LDS at the end; wave w
-// finishes dims [64w, 64w+64) and applies the sigmoid gate.  The gate is
-// loaded at the start as whole 16-byte row pieces and the output stored the
-// same way, both staged through the Q area of LDS, so neither goes out as
-// scattered 8-byte pieces.  With past == 0 the keys come from the key/value
+// finishes dims [64w, 64w+64) and applies the sigmoid gate.  Each wave loads
+// the gate of its quarter at the start as whole 128-byte lines and stores its
+// output the same way, both staged in its own part of the merge area, so
+// neither goes out as scattered 8-byte pieces and only one barrier follows
+// the loop.  With past == 0 the keys come from the key/value
 // inputs and each workgroup also writes its 8 tokens' cache rows (the append).
 #include "decode_scan.hpp"
 #include "prefill_mfma.hpp"
@@ -57,7 +58,8 @@ struct WaveTile {
 struct PrefillShared {
   union {
     WaveTile tile[kWaves];                  // 128 KiB
-    // merge: [finishing wave][source wave][block][register quad][lane]
+    // merge: [source wave][finishing wave][block][register quad][lane]; o[w][w]
+    // holds wave w's gate / output stage
     float4 o[kWaves][kWaves][2][4][kWave];
   };
   bf16_bits q[32 * kHeadDim]; // Q^T operand rows (one per column), swizzled like K
@@ -73,10 +75,6 @@ __device__ __forceinline__ int swz(int r) { return r & 7; }
 __device__ __forceinline__ int chunk_offset(int r, int c) { // in bf16 elements
   return r * kHeadDim + ((c ^ swz(r)) << 3);
 }
-
-// Gate / output staging in the Q area: element offset of 16-byte chunk k of
-// column row c.
-__device__ __forceinline__ int io_offset(int c, int k) { return c * kHeadDim + ((k ^ (c & 31)) << 3); }
 
 __device__ __forceinline__ bf16x8 lds_b128(const bf16_bits *p) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(p));
@@ -153,6 +151,12 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
   const std::size_t col_pos = past + t0 + col_row;
   const std::size_t col_head = kv_head * kGroup + (col >> 3);
   const int wave_u = __builtin_amdgcn_readfirstlane(wave); // wave index as a scalar
+  // Element offset of column c's row (head c / 8, token c % 8, clamped to the
+  // tile's tokens) in the query / gate / output layout [T][16][256].
+  auto io_row = [&](int c) {
+    const std::size_t tt = static_cast<std::size_t>(c & 7) < q_rows ? static_cast<std::size_t>(c & 7) : q_rows - 1;
+    return ((t0 + tt) * kQueryHeads + kv_head * kGroup + (c >> 3)) * kHeadDim;
+  };
   WaveTile &tile = sh.tile[wave_u];
   constexpr int kLateLoads = 4 + (FromInput ? 2 : 0); // gate (+ append) loads per thread
 
@@ -245,19 +249,17 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
       app[j] = *reinterpret_cast<const u32x4 *>(src + 8 * piece);
     }
   }
-  // Gate rows of this workgroup, held in registers until the epilogue: token
-  // tt's four heads are 2 KiB contiguous, read in 16-byte pieces (thread ->
-  // pieces tid + 256 j: token idx >> 7, piece idx & 127), so each load
-  // instruction covers whole 128-byte lines.  Rows past q_rows read row
-  // q_rows - 1 (never stored), so every thread issues exactly kLateLoads
-  // loads here, which the waits below count.
-  const std::size_t io_base = (t0 * kQueryHeads + kv_head * kGroup) * kHeadDim;
+  // Gate of this wave's output quarter (dims 64w .. 64w+63), held in registers
+  // until the epilogue.  Column c (head c / 8, token c % 8) of the quarter is
+  // one 128-byte line; load n covers columns 8n .. 8n+7 (lane -> column
+  // 8n + lane / 8, 16-byte chunk lane % 8), whole lines per instruction.
+  // Tokens past q_rows read token q_rows - 1 (never stored), so every thread
+  // issues exactly kLateLoads loads here, which the waits below count.
   u32x4 gc[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int idx = tid + kThreads * j, tt = idx >> 7, piece = idx & 127;
-    const std::size_t tr = static_cast<std::size_t>(tt) < q_rows ? tt : q_rows - 1;
-    gc[j] = *reinterpret_cast<const u32x4 *>(gate + io_base + tr * kQueryHeads * kHeadDim + 8 * piece);
+  for (int n = 0; n < 4; ++n) {
+    const int c = 8 * n + (lane >> 3), k = lane & 7;
+    gc[n] = *reinterpret_cast<const u32x4 *>(gate + io_row(c) + 64 * wave_u + 8 * k);
   }
 
   if (t < n_tiles) wait_vm<32 + kLateLoads>(); else wait_vm<0>(); // this wave's Q rows have landed
@@ -384,18 +386,12 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
                                    8 * piece) = app[j];
     }
   }
-  __syncthreads(); // every wave is done with its tile (and with Q)
-  // The gate goes to the Q area as [column][256] rows, 16-byte chunk k of row
-  // c at k ^ (c & 31): the epilogue's 8-byte reads (32 rows, one chunk) then
-  // hit distinct banks.
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int idx = tid + kThreads * j, tt = idx >> 7, piece = idx & 127;
-    const int c = (piece >> 5) * kQTok + tt;
-    *reinterpret_cast<u32x4 *>(sh.q + io_offset(c, piece & 31)) = gc[j];
-  }
-  // Wave w finishes O^T blocks 2w, 2w+1 (dims 64w .. 64w+63): it hands the
-  // other three quarters over through LDS and keeps its own in registers.
+  // Wave w finishes O^T blocks 2w, 2w+1 (dims 64w .. 64w+63).  As soon as its
+  // loop ends it writes the other three quarters into its own tile region
+  // (o[w][q] for finisher q; only wave w reads that region before this point),
+  // so early waves export while late ones still compute, and it stages its
+  // gate quarter in its own slot o[w][w].  One barrier, then each wave merges
+  // its quarter and finishes it without further workgroup synchronisation.
   // (The quarter loop is unrolled so that every register index is a
   // compile-time constant.)
 #pragma unroll
@@ -406,14 +402,24 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
         const floatx16 &x = o[2 * q + j];
-        sh.o[q][wave][j][i4][lane] = make_float4(x[4 * i4], x[4 * i4 + 1], x[4 * i4 + 2], x[4 * i4 + 3]);
+        sh.o[wave][q][j][i4][lane] = make_float4(x[4 * i4], x[4 * i4 + 1], x[4 * i4 + 2], x[4 * i4 + 3]);
       }
+  }
+  // Gate / output staging: [32 columns][64 dims] bf16 in the wave's own slot,
+  // 16-byte chunk k of column c at k ^ ((c / 4) % 8), so the epilogue's 8-byte
+  // reads (32 columns, one chunk) and the 16-byte row writes hit distinct banks.
+  bf16_bits *stage = reinterpret_cast<bf16_bits *>(&sh.o[wave][wave][0][0][0]);
+  auto stage_at = [](int c, int k) { return c * 64 + ((k ^ ((c >> 2) & 7)) << 3); };
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    const int c = 8 * n + (lane >> 3), k = lane & 7;
+    *reinterpret_cast<u32x4 *>(stage + stage_at(c, k)) = gc[n];
   }
   sh.m[wave][lane] = m_run;
   sh.l[wave][lane] = l_run;
-  __syncthreads();
+  __syncthreads(); // every wave's exports, m and l are written
 
-  // A wave that saw no key has m = -inf and weight 0; wave 0 always saw key 0.
+  // A wave that saw no key has m = -inf and weight 0; some wave saw key 0.
   float mw[kWaves], mm = -INFINITY;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
@@ -440,7 +446,7 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
-        const float4 x = sh.o[wave][w][j][i4][lane];
+        const float4 x = sh.o[w][wave][j][i4][lane];
         f[j][4 * i4] += a * x.x;
         f[j][4 * i4 + 1] += a * x.y;
         f[j][4 * i4 + 2] += a * x.z;
@@ -448,13 +454,14 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
       }
   }
   const float inv = 1.0f / (lsum + xor32(lsum));
-  // Gated outputs replace the gate in LDS (each lane rewrites exactly the
-  // 8-byte pieces it read), then go out as whole 16-byte row pieces.
+  // Gated outputs replace the gate in the stage (each lane rewrites exactly
+  // the 8-byte pieces it read: column col, dims 32 j + 8 i4 + 4 half of the
+  // quarter), then leave as whole 128-byte lines.
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
-      auto *slot = reinterpret_cast<u32x2 *>(sh.q + io_offset(col, 4 * (2 * wave + j) + i4) + 4 * half);
+      auto *slot = reinterpret_cast<u32x2 *>(stage + stage_at(col, 4 * j + i4) + 4 * half);
       const u32x2 g = *slot;
       const floatx16 &x = f[j];
       *slot = u32x2{pack_bf16x2(x[4 * i4] * inv * sigmoid_gate(bf16_lo(g[0])),
@@ -462,13 +469,13 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
                     pack_bf16x2(x[4 * i4 + 2] * inv * sigmoid_gate(bf16_lo(g[1])),
                                 x[4 * i4 + 3] * inv * sigmoid_gate(bf16_hi(g[1])))};
     }
-  __syncthreads();
+  wave_lds_order(); // the stage is rewritten by other lanes of this wave
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int idx = tid + kThreads * j, tt = idx >> 7, piece = idx & 127;
-    if (static_cast<std::size_t>(tt) < q_rows)
-      *reinterpret_cast<u32x4 *>(output + io_base + tt * kQueryHeads * kHeadDim + 8 * piece) =
-          *reinterpret_cast<const u32x4 *>(sh.q + io_offset((piece >> 5) * kQTok + tt, piece & 31));
+  for (int n = 0; n < 4; ++n) {
+    const int c = 8 * n + (lane >> 3), k = lane & 7;
+    if (static_cast<std::size_t>(c & 7) < q_rows)
+      *reinterpret_cast<u32x4 *>(output + io_row(c) + 64 * wave_u + 8 * k) =
+          *reinterpret_cast<const u32x4 *>(stage + stage_at(c, k));
   }
 }
 
