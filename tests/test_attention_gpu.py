@@ -215,6 +215,19 @@ def test_prefill_mfma_model_shape(gpu, T, past):
     assert np.array_equal(ck, keys) and np.array_equal(cv, vals)
 
 
+@pytest.mark.parametrize("past", [0, 1, 33])
+@pytest.mark.parametrize("T", [1, 2, 7, 9, 15, 31, 33, 63, 65, 100, 255, 257])
+def test_prefill_mfma_ragged_sweep(gpu, T, past):
+    # Ragged query tiles (T not a multiple of 8), partial last key tiles (past + T not a
+    # multiple of 32) and the diagonal mask at several offsets, on the bf16 MFMA path
+    # (with past == 0 the kernel also writes the cache rows itself).
+    out, expect, cache, keys, vals = run_prefill(3, 1, 1, T, HQ, HKV, D, past, seed=7 * T + past)
+    assert np.isfinite(out).all()
+    assert_bf16_close(out, bf16(expect), what=f"prefill T={T} past={past}")
+    ck, cv = read_cache(cache, 1, past + T, past + T)
+    assert np.array_equal(ck, keys) and np.array_equal(cv, vals)
+
+
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("act,cdt", [(1, 0), (1, 1), (3, 0), (3, 1)])
 @pytest.mark.parametrize("case", [(4, 4, 2, 64, 0), (17, 16, 4, 256, 0), (17, 16, 4, 256, 111),
