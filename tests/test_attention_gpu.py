@@ -131,6 +131,18 @@ def test_split_k_256_boundaries_and_partials(gpu, ctx):
     assert close_enough(pv[:, :active], ev.reshape(HQ, maxp, D)[:, :active])
 
 
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("ctx", [2, 33, 300, 1000, 2049, 3000])
+def test_split_k_256_layout_sweep(gpu, layout, ctx):
+    # Split-K 256 on the bf16 MFMA path in both cache layouts, odd contexts with a plan
+    # capacity above the active partitions (max_ctx 4096), device position, ~1% heavy rows.
+    out, expect, cache, keys, vals, *_ = run_decode(3, 1, layout, ctx, 4096, mode=2, seed=ctx + 31 * layout,
+                                                    heavy_rows=0.01)
+    assert_bf16_close(out, bf16(expect), what=f"split-256 layout {layout} ctx {ctx}")
+    ck, cv = read_cache(cache, layout, ctx, 4096)
+    assert np.array_equal(ck, keys) and np.array_equal(cv, vals)
+
+
 @pytest.mark.parametrize("ctx", [513, 777])
 def test_split_k_512(gpu, ctx):
     out, expect, *_ = run_decode(3, 1, 1, ctx, 1025, mode=3, seed=ctx + 5)
