@@ -106,3 +106,57 @@ def test_captured_decode_step_crosses_split_threshold(gpu):
         assert_bf16_close(from_dev(out).reshape(HQ, D), want, what=f"decode at context {p + 1}")
         ck = from_dev(cache)[: HKV * max_ctx * D].reshape(HKV, max_ctx, D)
         np.testing.assert_array_equal(ck[:, p], k_got)  # the appended row is the produced k
+
+
+def test_captured_prefill_and_delta_core_replay(gpu):
+    """The bf16 MFMA prefill (with its fused cache append) and the chunked gated-delta core
+    captured once each and replayed three times, with eager work and synchronizations between
+    the replays; every replay must reproduce the eager result bit for bit (the delta state is
+    restored eagerly before each replay)."""
+    gen = torch.Generator(device="cuda").manual_seed(77)
+    rnd = lambda *s: torch.randn(*s, device="cuda", generator=gen).to(torch.bfloat16)
+    T = 512
+    q, g, k, v = rnd(T, HQ, D), rnd(T, HQ, D), rnd(T, HKV, D), rnd(T, HKV, D)
+    cache = torch.zeros(2 * T * HKV * D, device="cuda", dtype=torch.bfloat16)
+    out = torch.empty(T, HQ, D, device="cuda", dtype=torch.bfloat16)
+    shape = ops.Qwen35AttentionShape(T, HQ, HKV, D, T, 0)
+    pol = ops.Qwen35AttentionLaunchPolicy(1, 1, 1)
+    run_prefill = lambda: ops.qwen35_causal_attention(q, k, v, g, out, cache, None, shape, 3, pol, stream=gpu)
+
+    dq = torch.nn.functional.normalize(torch.randn(T, 16, 128, device="cuda", generator=gen), dim=-1).to(torch.bfloat16)
+    dk = torch.nn.functional.normalize(torch.randn(T, 16, 128, device="cuda", generator=gen), dim=-1).to(torch.bfloat16)
+    dv = torch.randn(T, 32, 128, device="cuda", generator=gen).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(T, 32, device="cuda", generator=gen))
+    lg = -torch.nn.functional.softplus(torch.randn(T, 32, device="cuda", generator=gen))
+    s0 = torch.randn(32, 128, 128, device="cuda", generator=gen) * 0.05
+    st = s0.clone()
+    dout = torch.empty(T, 32, 128, device="cuda", dtype=torch.bfloat16)
+    ws = torch.empty(ops.qwen35_gated_delta_core_workspace_bytes(T, 16, 32, 128, 128), device="cuda",
+                     dtype=torch.uint8)
+    run_delta = lambda: ops.qwen35_gated_delta_core(dq, dk, dv, beta, lg, 128 ** -0.5, st, dout, ws, True,
+                                                    stream=gpu)
+
+    with torch.cuda.stream(gpu):
+        run_prefill()
+        run_delta()
+    torch.cuda.synchronize()
+    want_out, want_cache, want_dout, want_st = out.clone(), cache.clone(), dout.clone(), st.clone()
+
+    graph_p, graph_d = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph_p, stream=gpu):
+        run_prefill()
+    with torch.cuda.graph(graph_d, stream=gpu):
+        run_delta()
+    for replay in range(3):
+        out.zero_()
+        cache.zero_()
+        dout.zero_()
+        st.copy_(s0)
+        torch.cuda.synchronize()
+        graph_p.replay()
+        graph_d.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want_out), f"prefill replay {replay}"
+        assert torch.equal(cache, want_cache), f"prefill append replay {replay}"
+        assert torch.equal(dout, want_dout), f"delta output replay {replay}"
+        assert torch.equal(st, want_st), f"delta state replay {replay}"
