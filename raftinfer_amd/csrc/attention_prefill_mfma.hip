@@ -419,13 +419,40 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
   sh.l[wave][lane] = l_run;
   __syncthreads(); // every wave's exports, m and l are written
 
-  // A wave that saw no key has m = -inf and weight 0; some wave saw key 0.
-  float mw[kWaves], mm = -INFINITY;
+  // The other waves' quarters are read first; the gate's sigmoids (which do
+  // not depend on the merge) are computed while those reads are in flight.
+  float4 xo[kWaves][2][4];
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    if (w == wave) continue;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) xo[w][j][i4] = sh.o[w][wave][j][i4][lane];
+  }
+  float mw[kWaves], lw[kWaves];
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
     mw[w] = sh.m[w][lane];
-    mm = fmaxf(mm, mw[w]);
+    lw[w] = sh.l[w][lane];
   }
+  // Sigmoid of the gate pieces this lane finishes: column col, dims
+  // 32 j + 8 i4 + 4 half .. +3 of the quarter.
+  float sg[2][16];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const u32x2 g = *reinterpret_cast<const u32x2 *>(stage + stage_at(col, 4 * j + i4) + 4 * half);
+      sg[j][4 * i4] = sigmoid_gate(bf16_lo(g[0]));
+      sg[j][4 * i4 + 1] = sigmoid_gate(bf16_hi(g[0]));
+      sg[j][4 * i4 + 2] = sigmoid_gate(bf16_lo(g[1]));
+      sg[j][4 * i4 + 3] = sigmoid_gate(bf16_hi(g[1]));
+    }
+  // A wave that saw no key has m = -inf and weight 0; some wave saw key 0.
+  float mm = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, mw[w]);
   float lsum = 0.f;
   floatx16 f[2];
 #pragma unroll
@@ -440,13 +467,13 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
     const float a = fexp2(mw[w] - mm);
-    lsum += a * sh.l[w][lane];
+    lsum += a * lw[w];
     if (w == wave) continue;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
-        const float4 x = sh.o[w][wave][j][i4][lane];
+        const float4 x = xo[w][j][i4];
         f[j][4 * i4] += a * x.x;
         f[j][4 * i4 + 1] += a * x.y;
         f[j][4 * i4 + 2] += a * x.z;
@@ -455,19 +482,15 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
   }
   const float inv = 1.0f / (lsum + xor32(lsum));
   // Gated outputs replace the gate in the stage (each lane rewrites exactly
-  // the 8-byte pieces it read: column col, dims 32 j + 8 i4 + 4 half of the
-  // quarter), then leave as whole 128-byte lines.
+  // the 8-byte pieces it read), then leave as whole 128-byte lines.
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
       auto *slot = reinterpret_cast<u32x2 *>(stage + stage_at(col, 4 * j + i4) + 4 * half);
-      const u32x2 g = *slot;
       const floatx16 &x = f[j];
-      *slot = u32x2{pack_bf16x2(x[4 * i4] * inv * sigmoid_gate(bf16_lo(g[0])),
-                                x[4 * i4 + 1] * inv * sigmoid_gate(bf16_hi(g[0]))),
-                    pack_bf16x2(x[4 * i4 + 2] * inv * sigmoid_gate(bf16_lo(g[1])),
-                                x[4 * i4 + 3] * inv * sigmoid_gate(bf16_hi(g[1])))};
+      *slot = u32x2{pack_bf16x2(x[4 * i4] * inv * sg[j][4 * i4], x[4 * i4 + 1] * inv * sg[j][4 * i4 + 1]),
+                    pack_bf16x2(x[4 * i4 + 2] * inv * sg[j][4 * i4 + 2], x[4 * i4 + 3] * inv * sg[j][4 * i4 + 3])};
     }
   wave_lds_order(); // the stage is rewritten by other lanes of this wave
 #pragma unroll
