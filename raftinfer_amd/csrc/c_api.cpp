@@ -60,6 +60,12 @@ GatedDeltaLaunchPolicy to_delta_policy(raftinfer_amd_delta_policy p) {
           p.transposed_boundary_state != 0};
 }
 hipStream_t to_stream(void *s) { return static_cast<hipStream_t>(s); }
+// The result of a sizing / planning call is written through a caller pointer;
+// a null one is an invalid argument, not a crash.
+template <typename T> T &out_ref(T *p) {
+  if (p == nullptr) throw Qwen35PrimitiveError("raftinfer_amd result pointer is null");
+  return *p;
+}
 RaftInferDataType to_dtype(int d) { return static_cast<RaftInferDataType>(d); }
 
 } // namespace
@@ -69,18 +75,18 @@ extern "C" {
 const char *raftinfer_amd_last_error_message(void) { return g_last_error.c_str(); }
 
 int raftinfer_amd_attention_workspace_floats(raftinfer_amd_attention_shape shape, size_t *out) {
-  return guarded([&] { *out = qwen35_attention_workspace_floats(to_shape(shape)); });
+  return guarded([&] { out_ref(out) = qwen35_attention_workspace_floats(to_shape(shape)); });
 }
 
 int raftinfer_amd_attention_cache_bytes(raftinfer_amd_attention_shape shape,
                                         raftinfer_amd_attention_policy policy, size_t *out) {
-  return guarded([&] { *out = qwen35_attention_cache_bytes(to_shape(shape), to_policy(policy)); });
+  return guarded([&] { out_ref(out) = qwen35_attention_cache_bytes(to_shape(shape), to_policy(policy)); });
 }
 
 int raftinfer_amd_attention_workspace_bytes(raftinfer_amd_attention_shape shape,
                                             raftinfer_amd_attention_policy policy, size_t *out) {
   return guarded(
-      [&] { *out = qwen35_attention_workspace_bytes(to_shape(shape), to_policy(policy)); });
+      [&] { out_ref(out) = qwen35_attention_workspace_bytes(to_shape(shape), to_policy(policy)); });
 }
 
 int raftinfer_amd_online_decode_plan(raftinfer_amd_attention_shape shape, uint8_t requested,
@@ -88,7 +94,7 @@ int raftinfer_amd_online_decode_plan(raftinfer_amd_attention_shape shape, uint8_
   return guarded([&] {
     const auto p = qwen35_online_decode_plan(
         to_shape(shape), static_cast<Qwen35DecodeAttentionMode>(requested), context_tokens);
-    *out = {static_cast<uint8_t>(p.resolved_mode), p.partition_tokens,
+    out_ref(out) = {static_cast<uint8_t>(p.resolved_mode), p.partition_tokens,
             p.split_k_threshold_tokens, p.context_bucket_tokens, p.active_partition_capacity};
   });
 }
@@ -98,7 +104,7 @@ int raftinfer_amd_online_decode_workspace_layout(raftinfer_amd_attention_shape s
   return guarded([&] {
     const auto l = qwen35_online_decode_workspace_layout(
         to_shape(shape), static_cast<Qwen35DecodeAttentionMode>(resolved));
-    *out = {l.partial_count, l.max_offset_bytes, l.sum_offset_bytes, l.value_offset_bytes, l.bytes};
+    out_ref(out) = {l.partial_count, l.max_offset_bytes, l.sum_offset_bytes, l.value_offset_bytes, l.bytes};
   });
 }
 
@@ -110,21 +116,21 @@ int raftinfer_amd_online_attention_prefill_supported(raftinfer_amd_attention_sha
 }
 
 int raftinfer_amd_gated_delta_workspace_bytes(raftinfer_amd_delta_shape shape, size_t *out) {
-  return guarded([&] { *out = qwen35_gated_delta_workspace_bytes(to_delta(shape)); });
+  return guarded([&] { out_ref(out) = qwen35_gated_delta_workspace_bytes(to_delta(shape)); });
 }
 
 int raftinfer_amd_gated_delta_select_policy(raftinfer_amd_delta_shape shape, size_t bucket,
                                             raftinfer_amd_delta_policy *out) {
   return guarded([&] {
     const auto p = qwen35_gated_delta_select_policy(to_delta(shape), bucket);
-    *out = {static_cast<uint8_t>(p.schedule), p.warps_per_block,
+    out_ref(out) = {static_cast<uint8_t>(p.schedule), p.warps_per_block,
             static_cast<uint8_t>(p.transposed_boundary_state)};
   });
 }
 
 int raftinfer_amd_batched_decode_workspace_bytes(raftinfer_amd_batched_decode_shape s, size_t *out) {
   return guarded([&] {
-    *out = qwen35_batched_decode_workspace_bytes(
+    out_ref(out) = qwen35_batched_decode_workspace_bytes(
         {s.sequences, s.max_context_tokens, s.cache_stride_bytes, s.single_block_max_tokens});
   });
 }
@@ -232,7 +238,7 @@ int raftinfer_amd_online_attention_prefill_kernel_only(
 }
 
 int raftinfer_amd_consume_capacity_errors(uint32_t *out) {
-  return guarded([&] { *out = qwen35_online_attention_consume_capacity_errors(); });
+  return guarded([&] { out_ref(out) = qwen35_online_attention_consume_capacity_errors(); });
 }
 
 int raftinfer_amd_gated_delta(const void *input, const void *conv_weight, const void *a,
@@ -261,7 +267,7 @@ int raftinfer_amd_gated_delta_auto(const void *input, const void *conv_weight, c
 
 int raftinfer_amd_gated_delta_core_workspace_bytes(raftinfer_amd_delta_core_shape s, size_t *out) {
   return guarded([&] {
-    *out = qwen35_gated_delta_core_workspace_bytes(
+    out_ref(out) = qwen35_gated_delta_core_workspace_bytes(
         {s.tokens, s.key_heads, s.value_heads, s.key_dim, s.value_dim});
   });
 }

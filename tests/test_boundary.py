@@ -239,3 +239,17 @@ def test_pack_validation_errors_before_launch():
             ops.qwen35_pack_linear_delta_input(f, f, f, f, f, 1, *w, 3, stream=0x1234)
     with pytest.raises(ops.Qwen35PrimitiveError, match="width overflow"):
         ops.qwen35_pack_linear_delta_input(f, f, f, f, f, 1, 2 ** 64 - 2, 1, 1, 4, 3, stream=0x1234)
+
+
+def test_c_abi_null_result_pointer_is_an_invalid_argument():
+    # A sizing / planning call with a null result pointer returns an error status with a
+    # message instead of writing through it.
+    import ctypes
+    from raftinfer_amd import _lib
+    lib = _lib.load()
+    shape = _lib.AttentionShape(1, 16, 4, 256, 4096, 4095)
+    rc = lib.raftinfer_amd_attention_workspace_floats(shape, None)
+    assert rc == 1  # RAFTINFER_AMD_INVALID_ARGUMENT
+    assert b"result pointer is null" in lib.raftinfer_amd_last_error_message()
+    rc = lib.raftinfer_amd_gated_delta_core_workspace_bytes(_lib.DeltaCoreShape(512, 16, 32, 128, 128), None)
+    assert rc == 1
