@@ -78,6 +78,7 @@ void qwen35_online_attention_decode(const void *query, const void *key, const vo
 // Per-sequence policy: length <= single_block_max_tokens runs the
 // single-block path, otherwise split-K with 256-token partitions and an LSE
 // merge.  q/gate/out: [sequences][16][256]; k/v: [sequences][4][256].
+// query, kv_cache and workspace must be 16-byte aligned.
 struct Qwen35BatchedDecodeShape {
   std::size_t sequences;
   std::size_t max_context_tokens;

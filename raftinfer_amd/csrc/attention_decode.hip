@@ -195,9 +195,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_partition_kernel(
 }
 
 // Log-sum-exp merge over the active partitions of one query head plus the
-// sigmoid gate (cpp/kernels/qwen35_online_attention.cu:693-756).  The
-// partitions' max / sum are staged in LDS first so the value loads of all
-// partitions are independent.  A device position needing more partitions than
+// sigmoid gate (cpp/kernels/qwen35_online_attention.cu:693-756).  The value
+// loads of a chunk do not wait for its max / sum, so they are all independent.
+// A device position needing more partitions than
 // the plan's capacity writes NaN and counts a capacity error instead of
 // trapping.
 constexpr int kMergeChunk = 32;      // partitions per round trip (long contexts)
@@ -761,27 +761,114 @@ __global__ __launch_bounds__(256) void batched_append_kernel(const ActT *__restr
   cache[plane + idx] = f32_to_bf16(Elem<ActT>::load(value, src));
 }
 
-// Workgroup = (head, block of kMergeDims dims) of one sequence; thread = dim.
-// Chunks of 64 partitions: a 32768-token context (128 partitions) takes two
-// round trips.
+// Row merge for the batched path: the same log-sum-exp merge, laid out for
+// many partitions per head.  Workgroup = one head, W waves.  Wave w merges
+// partitions w, w+W, w+2W, ... online, in chunks of kRowChunk; lane l owns
+// dims 4l..4l+3, so every value load of a wave is one whole 1 KiB partial row
+// (the quarter-row loads of merge_head took twice as long on the same bytes
+// here).  The W waves' (max, sum, weighted row) then combine in LDS, thread d
+// finishing dim d.  At the 16 partitions of a 4096-token context the
+// 64-workgroup merge_head layout is faster (the call is latency-bound there).
+constexpr int kRowChunk = 16;
+constexpr int kBatchedMergeWaves = 8; // 128 partitions (32768 tokens) in one round trip
+
+template <int W> struct RowMergeShared {
+  float a[W][kHeadDim];
+  float m[W], l[W];
+};
+
+template <int W>
+__device__ __forceinline__ void merge_rows(const float *__restrict__ pmax,
+                                           const float *__restrict__ psum,
+                                           const float *__restrict__ pval, std::size_t first,
+                                           std::size_t active, RowMergeShared<W> &sh) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const std::size_t mine_total =
+      active > static_cast<std::size_t>(wave) ? (active - wave + W - 1) / W : 0;
+  const std::size_t own = first + wave;
+  float m = -INFINITY, l = 0.f;
+  float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (std::size_t base = 0; base < mine_total; base += kRowChunk) {
+    const std::size_t n = mine_total - base < kRowChunk ? mine_total - base : kRowChunk;
+    const std::size_t pl = own + W * (base + (static_cast<std::size_t>(lane) < n ? lane : n - 1));
+    const float mraw = pmax[pl];
+    const float sraw = psum[pl];
+    float4 vx[kRowChunk];
+#pragma unroll
+    for (int u = 0; u < kRowChunk; ++u) {
+      const std::size_t p = own + W * (base + (static_cast<std::size_t>(u) < n ? u : n - 1));
+      vx[u] = reinterpret_cast<const float4 *>(pval + p * kHeadDim)[lane];
+    }
+    const bool mine = static_cast<std::size_t>(lane) < n;
+    const float ml = mine ? mraw : -INFINITY;
+    const float cm = fmaxf(m, max_xor32(max_xor16(row16_max(ml))));
+    const float r = __expf(m - cm); // m = -inf on the first chunk -> 0
+    const float w = mine ? __expf(ml - cm) : 0.f;
+    l = fmaf(l, r, sum_xor32(sum_xor16(row16_sum(sraw * w))));
+    a.x *= r;
+    a.y *= r;
+    a.z *= r;
+    a.w *= r;
+#pragma unroll
+    for (int u = 0; u < kRowChunk; ++u) {
+      if (static_cast<std::size_t>(u) < n) {
+        const float wu =
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), u));
+        a.x = fmaf(vx[u].x, wu, a.x);
+        a.y = fmaf(vx[u].y, wu, a.y);
+        a.z = fmaf(vx[u].z, wu, a.z);
+        a.w = fmaf(vx[u].w, wu, a.w);
+      }
+    }
+    m = cm;
+  }
+  reinterpret_cast<float4 *>(sh.a[wave])[lane] = a;
+  if (lane == 0) {
+    sh.m[wave] = m;
+    sh.l[wave] = l;
+  }
+}
+
+// After merge_rows and a barrier: the merged, normalised value of dim d.  A
+// wave without partitions left max -inf, sum 0 and a zero row; it weighs 0.
+template <int W>
+__device__ __forceinline__ float combine_rows(const RowMergeShared<W> &sh, int d) {
+  float mm = sh.m[0];
+#pragma unroll
+  for (int v = 1; v < W; ++v) mm = fmaxf(mm, sh.m[v]);
+  float lt = 0.f, at = 0.f;
+#pragma unroll
+  for (int v = 0; v < W; ++v) {
+    const float e = sh.m[v] == -INFINITY ? 0.f : __expf(sh.m[v] - mm);
+    lt = fmaf(sh.l[v], e, lt);
+    at = fmaf(sh.a[v][d], e, at);
+  }
+  return at / lt;
+}
+
+// Workgroup = (sequence, head), kBatchedMergeWaves waves, so a 32768-token
+// context (128 partitions) takes one round trip.
 template <typename ActT>
-__global__ __launch_bounds__(kMergeDims) void batched_merge_kernel(
+__global__ __launch_bounds__(kBatchedMergeWaves * 64) void batched_merge_kernel(
     const ActT *__restrict__ gate, ActT *__restrict__ output, const float *__restrict__ pmax,
     const float *__restrict__ psum, const float *__restrict__ pval,
     const std::uint32_t *__restrict__ lengths, std::size_t max_ctx, std::size_t max_partitions,
     std::size_t single_max) {
+  __shared__ RowMergeShared<kBatchedMergeWaves> sh;
   const std::size_t seq = blockIdx.y;
-  const std::size_t head = blockIdx.x / (kHeadDim / kMergeDims);
-  const int d = static_cast<int>(blockIdx.x % (kHeadDim / kMergeDims)) * kMergeDims + threadIdx.x;
+  const std::size_t head = blockIdx.x;
   const std::size_t ctx = lengths[seq];
   if (ctx == 0 || ctx > max_ctx || ctx <= single_max) return;
   const std::size_t active = ctx / kBatchedPartition + (ctx % kBatchedPartition ? 1 : 0);
+  const int d = threadIdx.x & (kHeadDim - 1);
+  const bool finisher = threadIdx.x < kHeadDim;
   const std::size_t out_idx = (seq * kQueryHeads + head) * kHeadDim + d;
-  const float gv = Elem<ActT>::load(gate, out_idx);
-  float l, a;
-  merge_head<kMergeChunkLong>(d, pmax, psum, pval, (seq * kQueryHeads + head) * max_partitions,
-                              active, l, a);
-  Elem<ActT>::store(output, out_idx, (a / l) * sigmoid_gate(gv));
+  const float gv = finisher ? Elem<ActT>::load(gate, out_idx) : 0.f;
+  merge_rows<kBatchedMergeWaves>(pmax, psum, pval, (seq * kQueryHeads + head) * max_partitions,
+                                 active, sh);
+  __syncthreads();
+  if (finisher)
+    Elem<ActT>::store(output, out_idx, combine_rows<kBatchedMergeWaves>(sh, d) * sigmoid_gate(gv));
 }
 
 // bf16 batched path: MFMA scores, dims-sliced workgroups, fused append.
@@ -880,7 +967,7 @@ void launch_batched(const void *query, const void *key, const void *value, const
             q, k, v, g, out, base, shape.cache_stride_bytes, shape.max_context_tokens, lengths,
             max_partitions, shape.single_block_max_tokens, pmax, psum, pval);
     check_launch<Err>("qwen35_batched_decode_partition");
-    batched_merge_kernel<ActT><<<dim3(kQueryHeads * (kHeadDim / kMergeDims), seqs), kMergeDims, 0, stream>>>(
+    batched_merge_kernel<ActT><<<dim3(kQueryHeads, seqs), kBatchedMergeWaves * 64, 0, stream>>>(
         g, out, pmax, psum, pval, lengths, shape.max_context_tokens, max_partitions,
         shape.single_block_max_tokens);
     check_launch<Err>("qwen35_batched_decode_merge");
@@ -895,7 +982,7 @@ void launch_batched(const void *query, const void *key, const void *value, const
       q, k, v, g, out, base, shape.cache_stride_bytes, shape.max_context_tokens, lengths,
       max_partitions, shape.single_block_max_tokens, pmax, psum, pval);
   check_launch<Err>("qwen35_batched_decode_partition");
-  batched_merge_kernel<ActT><<<dim3(kQueryHeads * (kHeadDim / kMergeDims), seqs), kMergeDims, 0, stream>>>(
+  batched_merge_kernel<ActT><<<dim3(kQueryHeads, seqs), kBatchedMergeWaves * 64, 0, stream>>>(
       g, out, pmax, psum, pval, lengths, shape.max_context_tokens, max_partitions,
       shape.single_block_max_tokens);
   check_launch<Err>("qwen35_batched_decode_merge");
@@ -944,6 +1031,7 @@ void qwen35_online_attention_decode_batched(const void *query, const void *key,
                "batched decode grid overflow");
   require_aligned16(query, "batched decode query must be 16-byte aligned");
   require_aligned16(kv_cache, "batched decode KV cache must be 16-byte aligned");
+  require_aligned16(workspace, "batched decode workspace must be 16-byte aligned");
   if (act == RAFTINFER_DTYPE_F32)
     launch_batched<float>(query, key, value, gate, output, kv_cache, context_lengths, workspace,
                           shape, stream);

@@ -253,3 +253,16 @@ def test_c_abi_null_result_pointer_is_an_invalid_argument():
     assert b"result pointer is null" in lib.raftinfer_amd_last_error_message()
     rc = lib.raftinfer_amd_gated_delta_core_workspace_bytes(_lib.DeltaCoreShape(512, 16, 32, 128, 128), None)
     assert rc == 1
+
+
+def test_batched_decode_requires_aligned_workspace():
+    # The batched merge reads whole partial rows with 16-byte loads.
+    big = FakeTensor(nbytes=1 << 40)
+    lens = FakeTensor(addr=0x200000)
+    q = FakeTensor(nbytes=1 << 40, addr=0x300000)
+    q.shape = (2, 16, 256)
+    stride = 2 * 4 * 1024 * 256 * 2
+    with pytest.raises(ops.Qwen35PrimitiveError, match="workspace must be 16-byte aligned"):
+        ops.qwen35_online_attention_decode_batched(
+            q, big, big, big, big, big, lens, FakeTensor(nbytes=1 << 40, addr=0x400004), 1024,
+            stride, stream=0x1234)
