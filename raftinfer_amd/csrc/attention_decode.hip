@@ -200,9 +200,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_partition_kernel(
 // A device position needing more partitions than
 // the plan's capacity writes NaN and counts a capacity error instead of
 // trapping.
-constexpr int kMergeChunk = 32;      // partitions per round trip (long contexts)
-constexpr int kMergeChunkShort = 16; // when the plan's capacity is at most 16 partitions
-constexpr int kMergeChunkLong = 64;  // when it is at most 64 (one round trip up to ctx 16384 at P=256)
+constexpr int kMergeChunkShort = 16; // partitions per round trip (capacity at most 16)
 constexpr int kMergeDims = 64;       // dims per merge workgroup (one thread each)
 
 // Merges the partials of one head online over chunks of CH partitions;
@@ -211,7 +209,7 @@ constexpr int kMergeDims = 64;       // dims per merge workgroup (one thread eac
 // sums are lane reductions, and lane u's weight reaches the other lanes by
 // v_readlane.  Every load of a chunk is issued before any is used, so a
 // chunk costs one memory round trip.
-template <int CH = kMergeChunk>
+template <int CH>
 __device__ __forceinline__ void merge_head(int d, const float *__restrict__ pmax,
                                            const float *__restrict__ psum,
                                            const float *__restrict__ pval, std::size_t first,
@@ -247,7 +245,7 @@ __device__ __forceinline__ void merge_head(int d, const float *__restrict__ pmax
   a_out = a;
 }
 
-template <typename ActT, int CH = kMergeChunk>
+template <typename ActT, int CH>
 __global__ __launch_bounds__(kMergeDims) void decode_merge_kernel(
     const ActT *__restrict__ gate, ActT *__restrict__ output, const float *__restrict__ pmax,
     const float *__restrict__ psum, const float *__restrict__ pval, std::size_t max_ctx,
@@ -271,6 +269,119 @@ __global__ __launch_bounds__(kMergeDims) void decode_merge_kernel(
   float l, a;
   merge_head<CH>(d, pmax, psum, pval, head * max_partitions, active, l, a);
   Elem<ActT>::store(output, out_idx, (a / l) * sigmoid_gate(gv));
+}
+
+// Row merge for plans of more than 16 partitions and for the batched path:
+// the same log-sum-exp merge, laid out for many partitions per head.  Workgroup = one head, W waves.  Wave w merges
+// partitions w, w+W, w+2W, ... online, in chunks of kRowChunk; lane l owns
+// dims 4l..4l+3, so every value load of a wave is one whole 1 KiB partial row
+// (the quarter-row loads of merge_head took twice as long on the same bytes
+// here).  The W waves' (max, sum, weighted row) then combine in LDS, thread d
+// finishing dim d.  At 16 partitions (a 4096-token context) the 64-workgroup
+// merge_head layout is faster: the call is latency-bound there.
+constexpr int kRowChunk = 16;
+constexpr int kBatchedMergeWaves = 8; // 128 partitions (32768 tokens) in one round trip
+constexpr int kLongMergeWaves = 8;    // split-K merge of more than 16 partitions
+
+template <int W> struct RowMergeShared {
+  float a[W][kHeadDim];
+  float m[W], l[W];
+};
+
+template <int W>
+__device__ __forceinline__ void merge_rows(const float *__restrict__ pmax,
+                                           const float *__restrict__ psum,
+                                           const float *__restrict__ pval, std::size_t first,
+                                           std::size_t active, RowMergeShared<W> &sh) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const std::size_t mine_total =
+      active > static_cast<std::size_t>(wave) ? (active - wave + W - 1) / W : 0;
+  const std::size_t own = first + wave;
+  float m = -INFINITY, l = 0.f;
+  float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (std::size_t base = 0; base < mine_total; base += kRowChunk) {
+    const std::size_t n = mine_total - base < kRowChunk ? mine_total - base : kRowChunk;
+    const std::size_t pl = own + W * (base + (static_cast<std::size_t>(lane) < n ? lane : n - 1));
+    const float mraw = pmax[pl];
+    const float sraw = psum[pl];
+    float4 vx[kRowChunk];
+#pragma unroll
+    for (int u = 0; u < kRowChunk; ++u) {
+      const std::size_t p = own + W * (base + (static_cast<std::size_t>(u) < n ? u : n - 1));
+      vx[u] = reinterpret_cast<const float4 *>(pval + p * kHeadDim)[lane];
+    }
+    const bool mine = static_cast<std::size_t>(lane) < n;
+    const float ml = mine ? mraw : -INFINITY;
+    const float cm = fmaxf(m, max_xor32(max_xor16(row16_max(ml))));
+    const float r = __expf(m - cm); // m = -inf on the first chunk -> 0
+    const float w = mine ? __expf(ml - cm) : 0.f;
+    l = fmaf(l, r, sum_xor32(sum_xor16(row16_sum(sraw * w))));
+    a.x *= r;
+    a.y *= r;
+    a.z *= r;
+    a.w *= r;
+#pragma unroll
+    for (int u = 0; u < kRowChunk; ++u) {
+      if (static_cast<std::size_t>(u) < n) {
+        const float wu =
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), u));
+        a.x = fmaf(vx[u].x, wu, a.x);
+        a.y = fmaf(vx[u].y, wu, a.y);
+        a.z = fmaf(vx[u].z, wu, a.z);
+        a.w = fmaf(vx[u].w, wu, a.w);
+      }
+    }
+    m = cm;
+  }
+  reinterpret_cast<float4 *>(sh.a[wave])[lane] = a;
+  if (lane == 0) {
+    sh.m[wave] = m;
+    sh.l[wave] = l;
+  }
+}
+
+// After merge_rows and a barrier: the merged, normalised value of dim d.  A
+// wave without partitions left max -inf, sum 0 and a zero row; it weighs 0.
+template <int W>
+__device__ __forceinline__ float combine_rows(const RowMergeShared<W> &sh, int d) {
+  float mm = sh.m[0];
+#pragma unroll
+  for (int v = 1; v < W; ++v) mm = fmaxf(mm, sh.m[v]);
+  float lt = 0.f, at = 0.f;
+#pragma unroll
+  for (int v = 0; v < W; ++v) {
+    const float e = sh.m[v] == -INFINITY ? 0.f : __expf(sh.m[v] - mm);
+    lt = fmaf(sh.l[v], e, lt);
+    at = fmaf(sh.a[v][d], e, at);
+  }
+  return at / lt;
+}
+
+template <typename ActT, int W>
+__global__ __launch_bounds__(W * 64) void decode_merge_rows_kernel(
+    const ActT *__restrict__ gate, ActT *__restrict__ output, const float *__restrict__ pmax,
+    const float *__restrict__ psum, const float *__restrict__ pval, std::size_t max_ctx,
+    std::size_t host_position, std::size_t partition_tokens, std::size_t max_partitions,
+    std::size_t capacity, std::size_t threshold, const std::uint32_t *device_position) {
+  __shared__ RowMergeShared<W> sh;
+  const std::size_t position = read_position(device_position, host_position);
+  if (position >= max_ctx) return;
+  const std::size_t ctx = position + 1;
+  if (ctx < threshold) return;
+  const std::size_t active = ctx / partition_tokens + (ctx % partition_tokens ? 1 : 0);
+  const std::size_t head = blockIdx.x;
+  const int d = threadIdx.x & (kHeadDim - 1);
+  const std::size_t out_idx = head * kHeadDim + d;
+  const bool finisher = threadIdx.x < kHeadDim;
+  if (active > capacity) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&g_capacity_errors, 1u);
+    if (finisher) Elem<ActT>::store(output, out_idx, __builtin_nanf(""));
+    return;
+  }
+  const float gv = finisher ? Elem<ActT>::load(gate, out_idx) : 0.f;
+  merge_rows<W>(pmax, psum, pval, head * max_partitions, active, sh);
+  __syncthreads();
+  if (finisher) Elem<ActT>::store(output, out_idx, combine_rows<W>(sh, d) * sigmoid_gate(gv));
 }
 
 // ---- bf16 activations + bf16 cache: MFMA scores, dims-sliced workgroups.
@@ -373,9 +484,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_mfma_kernel(
 
 // ------------------------------------------------------------ launchers
 
-// The merge reads every active partition in one round trip per chunk; the
-// chunk is the smallest of 16, 64 or 32 (the general case) that holds the
-// plan's capacity in one round trip.
+// Plans of at most 16 partitions (ctx 4096 at P=256) use the 64-workgroup
+// quarter-row merge, which is latency-bound there; longer plans use the
+// 8-wave row merge, which reads whole partial rows and holds 128 partitions
+// in one round trip (ctx 16384: 20.9 -> 19.8 us per call).
 template <typename ActT>
 void launch_merge(const ActT *g, ActT *out, const float *pmax, const float *psum, const float *pval,
                   Qwen35AttentionShape shape, Qwen35OnlineDecodePlan plan, std::size_t max_partitions,
@@ -385,12 +497,8 @@ void launch_merge(const ActT *g, ActT *out, const float *pmax, const float *psum
     decode_merge_kernel<ActT, kMergeChunkShort><<<grid, kMergeDims, 0, stream>>>(
         g, out, pmax, psum, pval, shape.max_context_tokens, shape.past_tokens, plan.partition_tokens,
         max_partitions, plan.active_partition_capacity, plan.split_k_threshold_tokens, device_position);
-  else if (plan.active_partition_capacity <= static_cast<std::size_t>(kMergeChunkLong))
-    decode_merge_kernel<ActT, kMergeChunkLong><<<grid, kMergeDims, 0, stream>>>(
-        g, out, pmax, psum, pval, shape.max_context_tokens, shape.past_tokens, plan.partition_tokens,
-        max_partitions, plan.active_partition_capacity, plan.split_k_threshold_tokens, device_position);
   else
-    decode_merge_kernel<ActT, kMergeChunk><<<grid, kMergeDims, 0, stream>>>(
+    decode_merge_rows_kernel<ActT, kLongMergeWaves><<<kQueryHeads, kLongMergeWaves * 64, 0, stream>>>(
         g, out, pmax, psum, pval, shape.max_context_tokens, shape.past_tokens, plan.partition_tokens,
         max_partitions, plan.active_partition_capacity, plan.split_k_threshold_tokens, device_position);
 }
@@ -602,6 +710,7 @@ void decode_impl(const void *query, const void *key, const void *value, const vo
   if (ws.bytes != 0) {
     require<Err>(workspace != nullptr, "split-K online decode workspace is null");
     require<Err>(workspace_bytes >= ws.bytes, "split-K online decode workspace is too small");
+    require_aligned16(workspace, "split-K online decode workspace must be 16-byte aligned");
   }
   const std::size_t eb = cache_element_bytes_of(cache_dtype);
   require<Err>(eb != 0, "unsupported online attention KV cache dtype");
@@ -759,91 +868,6 @@ __global__ __launch_bounds__(256) void batched_append_kernel(const ActT *__restr
   const std::size_t src = seq * kKvHeads * kHeadDim + e;
   cache[idx] = f32_to_bf16(Elem<ActT>::load(key, src));
   cache[plane + idx] = f32_to_bf16(Elem<ActT>::load(value, src));
-}
-
-// Row merge for the batched path: the same log-sum-exp merge, laid out for
-// many partitions per head.  Workgroup = one head, W waves.  Wave w merges
-// partitions w, w+W, w+2W, ... online, in chunks of kRowChunk; lane l owns
-// dims 4l..4l+3, so every value load of a wave is one whole 1 KiB partial row
-// (the quarter-row loads of merge_head took twice as long on the same bytes
-// here).  The W waves' (max, sum, weighted row) then combine in LDS, thread d
-// finishing dim d.  At the 16 partitions of a 4096-token context the
-// 64-workgroup merge_head layout is faster (the call is latency-bound there).
-constexpr int kRowChunk = 16;
-constexpr int kBatchedMergeWaves = 8; // 128 partitions (32768 tokens) in one round trip
-
-template <int W> struct RowMergeShared {
-  float a[W][kHeadDim];
-  float m[W], l[W];
-};
-
-template <int W>
-__device__ __forceinline__ void merge_rows(const float *__restrict__ pmax,
-                                           const float *__restrict__ psum,
-                                           const float *__restrict__ pval, std::size_t first,
-                                           std::size_t active, RowMergeShared<W> &sh) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const std::size_t mine_total =
-      active > static_cast<std::size_t>(wave) ? (active - wave + W - 1) / W : 0;
-  const std::size_t own = first + wave;
-  float m = -INFINITY, l = 0.f;
-  float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (std::size_t base = 0; base < mine_total; base += kRowChunk) {
-    const std::size_t n = mine_total - base < kRowChunk ? mine_total - base : kRowChunk;
-    const std::size_t pl = own + W * (base + (static_cast<std::size_t>(lane) < n ? lane : n - 1));
-    const float mraw = pmax[pl];
-    const float sraw = psum[pl];
-    float4 vx[kRowChunk];
-#pragma unroll
-    for (int u = 0; u < kRowChunk; ++u) {
-      const std::size_t p = own + W * (base + (static_cast<std::size_t>(u) < n ? u : n - 1));
-      vx[u] = reinterpret_cast<const float4 *>(pval + p * kHeadDim)[lane];
-    }
-    const bool mine = static_cast<std::size_t>(lane) < n;
-    const float ml = mine ? mraw : -INFINITY;
-    const float cm = fmaxf(m, max_xor32(max_xor16(row16_max(ml))));
-    const float r = __expf(m - cm); // m = -inf on the first chunk -> 0
-    const float w = mine ? __expf(ml - cm) : 0.f;
-    l = fmaf(l, r, sum_xor32(sum_xor16(row16_sum(sraw * w))));
-    a.x *= r;
-    a.y *= r;
-    a.z *= r;
-    a.w *= r;
-#pragma unroll
-    for (int u = 0; u < kRowChunk; ++u) {
-      if (static_cast<std::size_t>(u) < n) {
-        const float wu =
-            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), u));
-        a.x = fmaf(vx[u].x, wu, a.x);
-        a.y = fmaf(vx[u].y, wu, a.y);
-        a.z = fmaf(vx[u].z, wu, a.z);
-        a.w = fmaf(vx[u].w, wu, a.w);
-      }
-    }
-    m = cm;
-  }
-  reinterpret_cast<float4 *>(sh.a[wave])[lane] = a;
-  if (lane == 0) {
-    sh.m[wave] = m;
-    sh.l[wave] = l;
-  }
-}
-
-// After merge_rows and a barrier: the merged, normalised value of dim d.  A
-// wave without partitions left max -inf, sum 0 and a zero row; it weighs 0.
-template <int W>
-__device__ __forceinline__ float combine_rows(const RowMergeShared<W> &sh, int d) {
-  float mm = sh.m[0];
-#pragma unroll
-  for (int v = 1; v < W; ++v) mm = fmaxf(mm, sh.m[v]);
-  float lt = 0.f, at = 0.f;
-#pragma unroll
-  for (int v = 0; v < W; ++v) {
-    const float e = sh.m[v] == -INFINITY ? 0.f : __expf(sh.m[v] - mm);
-    lt = fmaf(sh.l[v], e, lt);
-    at = fmaf(sh.a[v][d], e, at);
-  }
-  return at / lt;
 }
 
 // Workgroup = (sequence, head), kBatchedMergeWaves waves, so a 32768-token
