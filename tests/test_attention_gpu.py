@@ -143,6 +143,14 @@ def test_split_k_256_layout_sweep(gpu, layout, ctx):
     assert np.array_equal(ck, keys) and np.array_equal(cv, vals)
 
 
+@pytest.mark.parametrize("ctx", [2, 300, 2049, 5000, 16384])
+def test_split_k_row_merge_sparse_waves(gpu, ctx):
+    # max_ctx 16384 gives a plan capacity of 64 partitions, so the 8-wave row merge runs;
+    # at ctx 2 and 300 (1-2 active partitions) most of its waves have no partition.
+    out, expect, *_ = run_decode(3, 1, 1, ctx, 16384, mode=2, seed=ctx + 7, heavy_rows=0.01)
+    assert_bf16_close(out, bf16(expect), what=f"row merge ctx {ctx}")
+
+
 @pytest.mark.parametrize("ctx", [513, 777])
 def test_split_k_512(gpu, ctx):
     out, expect, *_ = run_decode(3, 1, 1, ctx, 1025, mode=3, seed=ctx + 5)
