@@ -53,7 +53,9 @@ template <int VEC> struct VRow {
   std::uint32_t w[VEC / 2];
   __device__ __forceinline__ void load(const bf16_bits *p) {
     if constexpr (VEC == 8) {
-      const u32x4 x = *reinterpret_cast<const u32x4 *>(p);
+      // Each V slice is read by one workgroup only: a non-temporal load keeps
+      // it from displacing the K lines that sibling workgroups re-read.
+      const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
       w[0] = x[0]; w[1] = x[1]; w[2] = x[2]; w[3] = x[3];
     } else if constexpr (VEC == 4) {
       const u32x2 x = *reinterpret_cast<const u32x2 *>(p);
@@ -93,6 +95,10 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
                                                  std::size_t pos, DecodeMfmaShared<DS, WAVES, CT> &sh) {
   constexpr int DIMS = kHeadDim / DS;
   constexpr int G = CT / 8; // 8-token groups per chunk
+  // K is read non-temporally when at most 4 sibling workgroups share it
+  // (split-K: 4096 -> 9.7 us per call, batched x32: 406 -> 375 us); the 16
+  // single-block siblings need it to stay in L2 (7.1 -> 8.0 us otherwise).
+  constexpr bool kNtKeys = DS <= 4;
   using Map = PvMap<DIMS, CT>;
   constexpr int VEC = Map::VEC, DL = Map::DL, TL = Map::TL, TPL = Map::TPL;
   const int lane = threadIdx.x & 63;
@@ -141,7 +147,8 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
                                         : kplane + cache_row(a.head_major, tok, kv_head, a.max_ctx);
 #pragma unroll
       for (int line = 0; line < 4; ++line)
-        kr[g][line] = *reinterpret_cast<const u32x4 *>(row + line * 64 + seg * 8);
+        kr[g][line] = kNtKeys ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(row + line * 64 + seg * 8))
+                              : *reinterpret_cast<const u32x4 *>(row + line * 64 + seg * 8);
     }
     VRow<VEC> vv[TPL];
 #pragma unroll
