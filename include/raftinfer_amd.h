@@ -190,7 +190,8 @@ int raftinfer_amd_online_attention_prefill_kernel_only(
     void *kv_cache, size_t kv_cache_bytes, raftinfer_amd_attention_shape shape,
     int activation_dtype, uint8_t cache_dtype, uint8_t cache_layout, void *stream);
 /* Device capacity-guard counter (replaces the reference merge kernel's trap,
- * qwen35_online_attention.cu:714-717).  Synchronizes the device. */
+ * qwen35_online_attention.cu:714-717); also counts batched-decode sequences
+ * whose length is 0 or above the maximum context.  Synchronizes the device. */
 int raftinfer_amd_consume_capacity_errors(uint32_t *out);
 
 /* qwen35_delta.cuh:96-102 (qwen35_gated_delta with a policy). */

@@ -116,8 +116,11 @@ void qwen35_online_attention_prefill_kernel_only(
 // device-read position needs more partitions than the plan's capacity
 // (cpp/kernels/qwen35_online_attention.cu:714-717), this build writes NaN to
 // the affected heads, records the condition in a device flag and exits
-// normally.  Returns the number of such events since the last call and clears
-// the flag (synchronizes the current device).
+// normally; the new K/V row is still appended when the position is inside the
+// cache.  The batched decode counts a sequence whose length is 0 or above its
+// maximum context the same way (its output rows become NaN).  Returns the
+// number of such events since the last call and clears the flag
+// (synchronizes the current device).
 std::uint32_t qwen35_online_attention_consume_capacity_errors();
 
 } // namespace raftinfer::kernels

@@ -468,7 +468,14 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_mfma_kernel(
   const std::size_t end = ctx < begin + partition_tokens ? ctx : begin + partition_tokens;
   decode_mfma_scan<DS, WAVES, CT>(a, kv_head, dq, begin, end, position, sh);
   __syncthreads();
-  if (dq == 0 && position >= begin && position < end) append_rows(a, kv_head, position);
+  // The workgroup whose range holds the position appends the new row.  When a
+  // device position lies beyond the plan's capacity no workgroup holds it (the
+  // merge then reports the capacity error); the last partition appends it so
+  // the cache still receives the row, as the reference's separate append
+  // kernel guarantees (cpp/kernels/qwen35_online_attention.cu:936-945).
+  const bool owns_position = position >= begin && position < end;
+  const bool past_capacity = partition + 1 == capacity && position >= begin + partition_tokens;
+  if (dq == 0 && (owns_position || past_capacity)) append_rows(a, kv_head, position);
   for (int o = threadIdx.x; o < kGroup * DIMS; o += WAVES * 64) {
     const int h = o / DIMS, d = o % DIMS;
     float mm, l, acc;
@@ -882,11 +889,19 @@ __global__ __launch_bounds__(kBatchedMergeWaves * 64) void batched_merge_kernel(
   const std::size_t seq = blockIdx.y;
   const std::size_t head = blockIdx.x;
   const std::size_t ctx = lengths[seq];
-  if (ctx == 0 || ctx > max_ctx || ctx <= single_max) return;
-  const std::size_t active = ctx / kBatchedPartition + (ctx % kBatchedPartition ? 1 : 0);
   const int d = threadIdx.x & (kHeadDim - 1);
   const bool finisher = threadIdx.x < kHeadDim;
   const std::size_t out_idx = (seq * kQueryHeads + head) * kHeadDim + d;
+  // A length of 0 or above max_ctx (a negative int32 reads as a huge uint32)
+  // has no valid context: every other kernel skips the sequence, and here its
+  // output rows become NaN and the guard counter counts it once.
+  if (ctx == 0 || ctx > max_ctx) {
+    if (head == 0 && threadIdx.x == 0) atomicAdd(&g_capacity_errors, 1u);
+    if (finisher) Elem<ActT>::store(output, out_idx, __builtin_nanf(""));
+    return;
+  }
+  if (ctx <= single_max) return;
+  const std::size_t active = ctx / kBatchedPartition + (ctx % kBatchedPartition ? 1 : 0);
   const float gv = finisher ? Elem<ActT>::load(gate, out_idx) : 0.f;
   merge_rows<kBatchedMergeWaves>(pmax, psum, pval, (seq * kQueryHeads + head) * max_partitions,
                                  active, sh);

@@ -172,23 +172,58 @@ def test_single_block_equals_split(gpu):
 
 
 def test_capacity_guard_reports_instead_of_trapping(gpu):
-    # cpp/tests/qwen35_cuda_attention_test.cu:1103-1164 (there: a device trap).
+    # cpp/tests/qwen35_cuda_attention_test.cu:1103-1164 (there: a device trap).  The
+    # reference appends before attention (qwen35_online_attention.cu:936-945), so the
+    # new row must reach the cache even when the merge reports the capacity error.
     ops.consume_capacity_errors()
     max_ctx = 1024
     shape = S(1, HQ, HKV, D, max_ctx, 0)
     plan = ops.qwen35_online_decode_plan(shape, 2, 256)
     assert plan[3] == 512 and plan[4] == 2
     nbytes = ops.qwen35_online_decode_workspace_layout(shape, 2)[4]
+    r = rng(512)
+    k, v = bf16(normal(r, HKV, D)), bf16(normal(r, HKV, D))
     z = lambda n: torch.zeros(n, device="cuda", dtype=torch.bfloat16)
     out = z(HQ * D)
     cache = z(2 * max_ctx * HKV * D)
     ws = torch.zeros(nbytes, device="cuda", dtype=torch.uint8)
     pos = torch.tensor([512], device="cuda", dtype=torch.int32)
-    ops.qwen35_online_attention_decode(z(HQ * D), z(HKV * D), z(HKV * D), z(HQ * D), out, cache, ws,
-                                       shape, 3, 1, 1, plan=plan, device_position=pos)
+    ops.qwen35_online_attention_decode(z(HQ * D), to_dev(k, torch.bfloat16), to_dev(v, torch.bfloat16),
+                                       z(HQ * D), out, cache, ws, shape, 3, 1, 1, plan=plan,
+                                       device_position=pos)
     assert ops.consume_capacity_errors() == 1
     assert torch.isnan(out.float()).all()
+    ck, cv = read_cache(from_dev(cache), 1, max_ctx, max_ctx)
+    assert np.array_equal(ck[512], k) and np.array_equal(cv[512], v)
+    assert not ck[:512].any() and not ck[513:].any()  # no other row written
     assert ops.consume_capacity_errors() == 0
+
+
+@pytest.mark.parametrize("ctx", [33000, 40000])
+def test_split_k_row_merge_multi_chunk(gpu, ctx):
+    # max_ctx 40960: 160 partitions, so each of the row merge's 8 waves merges up to 20
+    # partitions in two chunks (the running max is rescaled across chunks and the second
+    # chunk is partial).  Heavy rows in early and late partitions move the max both ways.
+    past_k, past_v, q, k, v, g = decode_inputs(ctx, ctx)
+    past_k[5] *= 8.0
+    past_k[ctx - 300] *= 8.0
+    past_k[ctx // 2] *= 8.0
+    max_ctx = 40960
+    cache = to_dev(bf16(make_cache(past_k, past_v, 1, max_ctx)), torch.bfloat16)
+    qa, ka, va, ga = (bf16(x) for x in (q, k, v, g))
+    shape = S(1, HQ, HKV, D, max_ctx, ctx - 1)
+    plan = ops.qwen35_online_decode_plan(shape, 2, ctx)
+    assert plan[4] == 160
+    ws = torch.zeros(ops.qwen35_online_decode_workspace_layout(shape, 2)[4], device="cuda",
+                     dtype=torch.uint8)
+    out = torch.empty(HQ * D, device="cuda", dtype=torch.bfloat16)
+    ops.qwen35_online_attention_decode(*(to_dev(x, torch.bfloat16) for x in (qa, ka, va, ga)), out,
+                                       cache, ws, shape, 3, 1, 1, plan=plan)
+    torch.cuda.synchronize()
+    keys = bf16(np.concatenate([past_k, ka[None]]))
+    vals = bf16(np.concatenate([past_v, va[None]]))
+    expect = orc.attention_core(qa[None], keys, vals, ga[None], ctx - 1)[0]
+    assert_bf16_close(from_dev(out).reshape(HQ, D), bf16(expect), what=f"row merge ctx {ctx}")
 
 
 def prefill_case(act, cdt, layout, T, hq, hkv, d, past, seed, q_scale=1.0):
@@ -399,6 +434,47 @@ def test_batched_ragged_decode(gpu, lengths, max_ctx):
     got = from_dev(out)
     for b in range(B):
         assert_bf16_close(got[b], bf16(expects[b]), what=f"batched seq {b} len {lengths[b]}")
+
+
+@pytest.mark.parametrize("act", [1, 3])
+def test_batched_out_of_range_lengths_report_nan(gpu, act):
+    # Lengths 0, above max_ctx, and -1 (read as 0xFFFFFFFF) have no valid context: their
+    # output rows become NaN and each is counted once; the valid sequences are unaffected
+    # and no cache row of an invalid sequence is written.
+    ops.consume_capacity_errors()
+    lengths, max_ctx = [300, 0, 700, 1025, -1], 1024
+    B = len(lengths)
+    r = rng(99)
+    per = 2 * max_ctx * HKV * D
+    cache_np = np.zeros(B * per, np.float32)
+    q, g = bf16(normal(r, B, HQ, D)), bf16(normal(r, B, HQ, D))
+    k, v = bf16(normal(r, B, HKV, D)), bf16(normal(r, B, HKV, D))
+    expects = {}
+    for b, L in enumerate(lengths):
+        if not 0 < L <= max_ctx:
+            continue
+        pk, pv = bf16(normal(r, L - 1, HKV, D)), bf16(normal(r, L - 1, HKV, D))
+        cache_np[b * per:(b + 1) * per] = make_cache(pk, pv, 1, max_ctx)
+        expects[b] = orc.attention_core(q[b:b + 1], np.concatenate([pk, k[b:b + 1]]),
+                                        np.concatenate([pv, v[b:b + 1]]), g[b:b + 1], L - 1)[0]
+    cache = to_dev(cache_np, torch.bfloat16)
+    lens = torch.tensor(lengths, device="cuda", dtype=torch.int32)
+    ws = torch.empty(ops.qwen35_batched_decode_workspace_bytes(B, max_ctx, per * 2), device="cuda",
+                     dtype=torch.uint8)
+    out = torch.zeros(B, HQ, D, device="cuda", dtype=TDT[act])
+    t = lambda a: to_dev(a, TDT[act])
+    ops.qwen35_online_attention_decode_batched(t(q), t(k), t(v), t(g), out, cache, lens, ws,
+                                               max_ctx, per * 2, activation_dtype=act)
+    torch.cuda.synchronize()
+    got = from_dev(out)
+    assert ops.consume_capacity_errors() == 3
+    cache_out = from_dev(cache)
+    for b, L in enumerate(lengths):
+        if b in expects:
+            assert close_enough(got[b], expects[b]), f"seq {b}"
+        else:
+            assert np.isnan(got[b]).all(), f"seq {b}"
+            assert not cache_out[b * per:(b + 1) * per].any(), f"seq {b} cache written"
 
 
 def test_batched_ragged_decode_cfg4_full_size(gpu):

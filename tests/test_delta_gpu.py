@@ -205,3 +205,27 @@ def test_core_chunked_equals_recurrent(gpu):
     b_o, b_s = run_core(q, k, v, beta, g, s0, chunked=False)
     assert rel_l2(a_s, b_s) < 1e-4
     assert_bf16_close(a_o, b_o, what="chunked vs recurrent")
+
+
+def test_cfg5_full_entry_prefill_512_then_32_decode_steps(gpu):
+    # The drop-in qwen35_gated_delta (conv + SiLU + l2norm + chunked recurrence + out-norm,
+    # cpp/kernels/qwen35_delta.cu:811-897) at the benchmark's config-5 shape: a T=512 prefill
+    # from zero states, then 32 single-token calls continuing from the returned states,
+    # each against the oracle's token-sequential prefill (cpp/reference/qwen35.cpp:384-549).
+    sh = model_shape(512)
+    fx = fixture_for(sh, seed=5120)
+    got = run_gpu(sh, fx, 3, 3)
+    want = run_ref(sh, fx, 3, 3)
+    check(got, want)
+    assert rel_l2(got[2], want[2]) < 1e-4
+    assert rel_l2(got[0], want[0]) < 5e-3
+    g_conv, g_rec, w_conv, w_rec = got[1], got[2], want[1], want[2]
+    sh1 = model_shape(1)
+    for step in range(32):
+        f1 = fixture_for(sh1, seed=6000 + step)
+        f1["cw"], f1["a"], f1["dt"], f1["nw"] = fx["cw"], fx["a"], fx["dt"], fx["nw"]
+        go, g_conv, g_rec = run_gpu(sh1, f1, 3, 3, g_conv, g_rec)
+        wo, w_conv, w_rec = run_ref(sh1, f1, 3, 3, w_conv, w_rec)
+        assert close_enough(go, wo), f"decode step {step}"
+    assert rel_l2(g_rec, w_rec) < 1e-4
+    assert np.array_equal(g_conv, w_conv) or rel_l2(g_conv, w_conv) < 1e-6
