@@ -176,6 +176,20 @@ int raftinfer_amd_online_attention_decode_batched(
     void *kv_cache, size_t kv_cache_bytes, const uint32_t *context_lengths, void *workspace,
     size_t workspace_bytes, raftinfer_amd_batched_decode_shape shape, int activation_dtype,
     void *stream);
+/* Allocation-free decode.  No counterpart in the reference: for callers that
+ * cannot allocate device memory (HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  As raftinfer_amd_online_attention_decode
+ * with a plan, but the split-K workspace is a library-owned static device
+ * array of raftinfer_amd_online_attention_static_workspace_bytes() bytes per
+ * GPU (8,454,144: max_context_tokens <= 131072 at split_k_256, <= 262144 at
+ * split_k_512); larger plans return RAFTINFER_AMD_INVALID_ARGUMENT.  Calls
+ * that overlap on one GPU share that array and race. */
+size_t raftinfer_amd_online_attention_static_workspace_bytes(void);
+int raftinfer_amd_online_attention_decode_static_workspace(
+    const void *query, const void *key, const void *value, const void *gate, void *output,
+    void *kv_cache, size_t kv_cache_bytes, raftinfer_amd_attention_shape shape,
+    int activation_dtype, uint8_t cache_dtype, uint8_t cache_layout,
+    raftinfer_amd_decode_plan plan, const uint32_t *device_position, void *stream);
 /* Measurement entry points (no reference counterpart): validate like the
  * calls above, then enqueue only the dominant kernel (the split-K partition
  * kernel; the prefill attention kernel without the K/V append). */

@@ -95,6 +95,24 @@ void qwen35_online_attention_decode_batched(const void *query, const void *key,
                                             RaftInferDataType activation_dtype,
                                             hipStream_t stream);
 
+// Allocation-free decode (no counterpart in the reference): for callers that
+// cannot allocate device memory (code under HIP graph capture, tight serving
+// loops, harnesses that forbid hipMalloc).  Same arguments and behaviour as
+// qwen35_online_attention_decode with a plan, except that the split-K
+// workspace is a library-owned static device array of
+// qwen35_online_attention_static_workspace_bytes() bytes per GPU (8,454,144:
+// max_context_tokens <= 131072 at split_k_256, <= 262144 at split_k_512); a
+// larger plan is rejected with Qwen35PrimitiveError.  Nothing is allocated.
+// Every call on one GPU shares that array, so calls that overlap on one GPU
+// (different streams, or different host threads) race; serialize them.
+std::size_t qwen35_online_attention_static_workspace_bytes() noexcept;
+void qwen35_online_attention_decode_static_workspace(
+    const void *query, const void *key, const void *value, const void *gate, void *output,
+    void *kv_cache, std::size_t kv_cache_bytes, Qwen35AttentionShape shape,
+    RaftInferDataType activation_dtype, Qwen35KvCacheDType cache_dtype,
+    Qwen35KvCacheLayout cache_layout, Qwen35OnlineDecodePlan plan,
+    const std::uint32_t *device_position, hipStream_t stream);
+
 // Measurement entry points (no counterpart in the reference): validate
 // exactly like qwen35_online_attention_decode / _prefill, then enqueue only the
 // dominant kernel -- the split-K partition kernel of a split plan, or the

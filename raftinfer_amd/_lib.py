@@ -99,6 +99,9 @@ SIGNATURES = {
         ([_vp] * 6 + [_sz, _PU32, _vp, _sz, BatchedDecodeShape, _I, _vp], _I),
     "raftinfer_amd_online_attention_decode_partition_only":
         ([_vp] * 6 + [_sz, _vp, _sz, AttentionShape, _I, _u8, _u8, DecodePlan, _PU32, _vp], _I),
+    "raftinfer_amd_online_attention_static_workspace_bytes": ([], _sz),
+    "raftinfer_amd_online_attention_decode_static_workspace":
+        ([_vp] * 6 + [_sz, AttentionShape, _I, _u8, _u8, DecodePlan, _PU32, _vp], _I),
     "raftinfer_amd_online_attention_prefill_kernel_only":
         ([_vp] * 6 + [_sz, AttentionShape, _I, _u8, _u8, _vp], _I),
     "raftinfer_amd_consume_capacity_errors": ([_PU32], _I),

@@ -11,6 +11,7 @@
 #include "raftinfer_amd/qwen35_online_attention.hpp"
 
 #include <atomic>
+#include <mutex>
 
 namespace raftinfer::kernels {
 namespace {
@@ -788,6 +789,67 @@ void qwen35_online_attention_decode(const void *query, const void *key, const vo
   qwen35_online_attention_decode(query, key, value, gate, output, kv_cache, kv_cache_bytes,
                                  nullptr, 0, shape, act, cache_dtype, layout, plan,
                                  device_position, stream);
+}
+
+// ------------------------------------------- allocation-free decode
+// The split-K partials of the static-workspace entry point live in this
+// file-scope array: 16 query heads x 512 partitions x (max + sum + 256
+// values) fp32, i.e. a 131,072-token maximum context at P=256 (262,144 at
+// P=512).  Each GPU holds its own copy for the life of the process.  Host
+// code never uses the array's name as an address: the per-device address
+// comes from hipGetSymbolAddress.
+constexpr std::size_t kStaticWorkspaceBytes =
+    std::size_t{16} * 512 * (2 + 256) * sizeof(float); // 8,454,144
+static __device__ __align__(256) unsigned char scratch[kStaticWorkspaceBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up once per device with
+// that device current.
+void *scratch_for_current_device() {
+  int device = -1;
+  require<Err>(hipGetDevice(&device) == hipSuccess, "static decode workspace: hipGetDevice failed");
+  require<Err>(device >= 0 && device < kMaxDevices, "static decode workspace: device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[device] == nullptr) {
+    void *ptr = nullptr;
+    const hipError_t rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    require<Err>(rc == hipSuccess && ptr != nullptr,
+                 "static decode workspace: hipGetSymbolAddress failed");
+    g_scratch_ptr[device] = ptr;
+  }
+  return g_scratch_ptr[device];
+}
+} // namespace
+
+std::size_t qwen35_online_attention_static_workspace_bytes() noexcept {
+  return kStaticWorkspaceBytes;
+}
+
+void qwen35_online_attention_decode_static_workspace(
+    const void *query, const void *key, const void *value, const void *gate, void *output,
+    void *kv_cache, std::size_t kv_cache_bytes, Qwen35AttentionShape shape,
+    RaftInferDataType activation_dtype, Qwen35KvCacheDType cache_dtype,
+    Qwen35KvCacheLayout cache_layout, Qwen35OnlineDecodePlan plan,
+    const std::uint32_t *device_position, hipStream_t stream) {
+  require<Err>(plan.resolved_mode != Qwen35DecodeAttentionMode::auto_select,
+               "online decode plan mode must be resolved");
+  std::size_t bytes = 0;
+  if (partition_tokens_for_mode(plan.resolved_mode) != 0) {
+    require<Err>(model_signature(shape),
+                 "split-K online decode requires the Qwen3.5 model signature");
+    bytes = qwen35_online_decode_workspace_layout(shape, plan.resolved_mode).bytes;
+    require<Err>(bytes <= kStaticWorkspaceBytes,
+                 "static decode workspace is too small for this maximum context (at most "
+                 "131072 tokens at split_k_256, 262144 at split_k_512); pass a workspace to "
+                 "qwen35_online_attention_decode instead");
+  }
+  void *workspace = bytes != 0 ? scratch_for_current_device() : nullptr;
+  decode_impl(query, key, value, gate, output, kv_cache, kv_cache_bytes, workspace, bytes, shape,
+              activation_dtype, cache_dtype, cache_layout, plan, device_position, stream, false);
 }
 
 std::uint32_t qwen35_online_attention_consume_capacity_errors() {

@@ -225,6 +225,23 @@ int raftinfer_amd_online_attention_decode_partition_only(
   });
 }
 
+size_t raftinfer_amd_online_attention_static_workspace_bytes(void) {
+  return qwen35_online_attention_static_workspace_bytes();
+}
+
+int raftinfer_amd_online_attention_decode_static_workspace(
+    const void *q, const void *k, const void *v, const void *g, void *o, void *cache,
+    size_t cache_bytes, raftinfer_amd_attention_shape shape, int act, uint8_t cache_dtype,
+    uint8_t cache_layout, raftinfer_amd_decode_plan plan, const uint32_t *device_position,
+    void *stream) {
+  return guarded([&] {
+    qwen35_online_attention_decode_static_workspace(
+        q, k, v, g, o, cache, cache_bytes, to_shape(shape), to_dtype(act),
+        static_cast<Qwen35KvCacheDType>(cache_dtype), static_cast<Qwen35KvCacheLayout>(cache_layout),
+        to_plan(plan), device_position, to_stream(stream));
+  });
+}
+
 int raftinfer_amd_online_attention_prefill_kernel_only(
     const void *q, const void *k, const void *v, const void *g, void *o, void *cache,
     size_t cache_bytes, raftinfer_amd_attention_shape shape, int act, uint8_t cache_dtype,

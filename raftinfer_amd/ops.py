@@ -233,6 +233,23 @@ def qwen35_online_attention_decode(query, key, value, gate, output, kv_cache, wo
         _stream(stream)))
 
 
+def qwen35_online_attention_static_workspace_bytes() -> int:
+    return int(_lib.load().raftinfer_amd_online_attention_static_workspace_bytes())
+
+
+def qwen35_online_attention_decode_static_workspace(query, key, value, gate, output, kv_cache, shape,
+                                                    activation_dtype, cache_dtype, cache_layout,
+                                                    plan, device_position=None, stream=None) -> None:
+    """The allocation-free decode: as qwen35_online_attention_decode with a
+    plan, with the split-K workspace in the library's static device array."""
+    pos = None if device_position is None else ctypes.cast(device_position.data_ptr(),
+                                                           ctypes.POINTER(ctypes.c_uint32))
+    _call(Qwen35PrimitiveError, _lib.load().raftinfer_amd_online_attention_decode_static_workspace(
+        _ptr(query), _ptr(key), _ptr(value), _ptr(gate), _ptr(output), _ptr(kv_cache),
+        _nbytes(kv_cache), shape.c(), activation_dtype, cache_dtype, cache_layout, DecodePlan(*plan),
+        pos, _stream(stream)))
+
+
 def qwen35_online_attention_decode_batched(query, key, value, gate, output, kv_cache,
                                            context_lengths, workspace, max_context_tokens,
                                            cache_stride_bytes, single_block_max_tokens=512,
