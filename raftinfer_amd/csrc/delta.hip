@@ -345,6 +345,135 @@ __global__ __launch_bounds__(256) void conv_norm_fast_kernel(
   }
 }
 
+// Qwen3.5 shapes, spread over channels: workgroup (TT consecutive tokens,
+// 512-channel block), one wave, 8 channels per lane (a 128-channel head is one
+// 16-lane DPP row), so a one-token call still spans conv_dim / 512 CUs.
+// Input, weights and history are read as 16-byte vectors, every load of the
+// workgroup is issued before the first use, and the TT tokens slide one
+// window over their inputs (TT + 3 rows read for TT outputs).  With
+// kUpdateState (one token) the lane that reads a channel's history also writes
+// its shifted history, so no separate state update runs.  Same math as
+// conv_norm_kernel.
+constexpr int kConvWideChannels = 512;
+template <typename T, typename Wt, int W, int TT, bool kUpdateState>
+__global__ __launch_bounds__(64) void conv_norm_wide_kernel(
+    const T *__restrict__ input, const Wt *__restrict__ conv_w, float *__restrict__ conv_state,
+    const Wt *__restrict__ recurrent_a, const Wt *__restrict__ dt_bias, float *__restrict__ convolved,
+    float *__restrict__ beta, float *__restrict__ gdecay, std::size_t tokens, std::size_t stride,
+    std::size_t conv_dim, std::size_t qk_channels, std::size_t hv) {
+  constexpr int H = W - 1;
+  static_assert(H == 3, "history vectors assume a width-4 convolution");
+  static_assert(!kUpdateState || TT == 1, "the fused state update is for one-token calls");
+  const std::size_t t0 = static_cast<std::size_t>(blockIdx.x) * TT;
+  const std::size_t c = static_cast<std::size_t>(blockIdx.y) * kConvWideChannels + 8 * threadIdx.x;
+  // win[j]: the input row of extended index t0 + j, where extended indices
+  // 0..H-1 are the stored history and H + t is token t.
+  float win[H + TT][8], w[8 * W];
+#pragma unroll
+  for (int u = 0; u < TT; ++u) {
+    const std::size_t t = t0 + u < tokens ? t0 + u : tokens - 1;
+    load8(input + t * stride + c, win[H + u]);
+  }
+#pragma unroll
+  for (int j = 0; j < W; ++j) {
+    float x[8];
+    load8(conv_w + c * W + 8 * j, x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[8 * j + e] = x[e];
+  }
+  float hist[8 * H]; // history of channel c + e, slot s: conv_state[(c + e) * H + s]
+  if (t0 < static_cast<std::size_t>(H)) {
+    const float4 *hp = reinterpret_cast<const float4 *>(conv_state + c * H);
+#pragma unroll
+    for (int j = 0; j < 2 * H; ++j) {
+      const float4 v = hp[j];
+      hist[4 * j] = v.x; hist[4 * j + 1] = v.y; hist[4 * j + 2] = v.z; hist[4 * j + 3] = v.w;
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < H; ++h) {
+    const std::size_t src = t0 + h;
+    if (src < static_cast<std::size_t>(H)) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) win[h][e] = hist[e * H + static_cast<int>(src)];
+    } else {
+      load8(input + (src - H) * stride + c, win[h]);
+    }
+  }
+  const bool qk = c < qk_channels;
+  const float qscale = c < qk_channels / 2 ? 1.0f / sqrtf(static_cast<float>(kChunkDim)) : 1.0f;
+#pragma unroll
+  for (int u = 0; u < TT; ++u) {
+    if (t0 + u >= tokens) break;
+    float y[8], ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float sum = win[H + u][e] * w[e * W + H];
+#pragma unroll
+      for (int h = 0; h < H; ++h) sum += win[u + h][e] * w[e * W + h];
+      y[e] = silu(sum);
+      ss += y[e] * y[e];
+    }
+    if (qk) { // q or k head: L2 norm over its 128 channels
+      ss = row16_sum(ss);
+      const float scale = qscale / sqrtf(ss + kQkNormEpsilon);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] *= scale;
+    }
+    float *dst = convolved + (t0 + u) * conv_dim + c;
+    *reinterpret_cast<float4 *>(dst) = make_float4(y[0], y[1], y[2], y[3]);
+    *reinterpret_cast<float4 *>(dst + 4) = make_float4(y[4], y[5], y[6], y[7]);
+  }
+  if constexpr (kUpdateState) {
+    // one token: the new history of channel c + e is (slot 1, slot 2, cur)
+    float nh[8 * H];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      nh[e * H] = hist[e * H + 1];
+      nh[e * H + 1] = hist[e * H + 2];
+      nh[e * H + 2] = win[H][e];
+    }
+    float4 *hp = reinterpret_cast<float4 *>(conv_state + c * H);
+#pragma unroll
+    for (int j = 0; j < 2 * H; ++j) hp[j] = make_float4(nh[4 * j], nh[4 * j + 1], nh[4 * j + 2], nh[4 * j + 3]);
+  }
+  if (blockIdx.y == 0) {
+    for (int i = threadIdx.x; i < TT * static_cast<int>(hv); i += 64) {
+      const std::size_t t = t0 + i / hv, h = i % hv;
+      if (t >= tokens) break;
+      const float b = Elem<T>::load(input, t * stride + conv_dim + h);
+      const float a = Elem<T>::load(input, t * stride + conv_dim + hv + h);
+      beta[t * hv + h] = sigmoid(b);
+      gdecay[t * hv + h] = Elem<Wt>::load(recurrent_a, h) * softplus(a + Elem<Wt>::load(dt_bias, h));
+    }
+  }
+}
+
+// Shifts the convolution history of the channels this thread owns (channel
+// ch = first, first + step, ...): slot s becomes the input row of token
+// tokens - H + s, or the old slot s + tokens when that token precedes the call.
+// Runs in a kernel that starts after every read of the old history has
+// finished (a later launch on the same stream), and each channel has one
+// owner, so the update is race-free.
+template <int H, typename T>
+__device__ __forceinline__ void shift_conv_history(const T *__restrict__ input,
+                                                   float *__restrict__ conv_state,
+                                                   std::size_t tokens, std::size_t stride,
+                                                   std::size_t conv_dim, std::size_t first,
+                                                   std::size_t step) {
+  for (std::size_t ch = first; ch < conv_dim; ch += step) {
+    float nh[H];
+#pragma unroll
+    for (int s = 0; s < H; ++s) {
+      const std::size_t src = tokens + s; // extended index
+      nh[s] = src < static_cast<std::size_t>(H) ? conv_state[ch * H + src]
+                                                : Elem<T>::load(input, (src - H) * stride + ch);
+    }
+#pragma unroll
+    for (int s = 0; s < H; ++s) conv_state[ch * H + s] = nh[s];
+  }
+}
+
 // One block per token; a 128-wide value head is one 16-lane DPP row.
 template <typename T, typename Wt>
 __global__ __launch_bounds__(256) void out_norm_fast_kernel(const T *__restrict__ input,
@@ -352,9 +481,15 @@ __global__ __launch_bounds__(256) void out_norm_fast_kernel(const T *__restrict_
                                                             const float *__restrict__ raw,
                                                             T *__restrict__ output,
                                                             std::size_t stride, std::size_t conv_dim,
-                                                            std::size_t hv, float eps) {
+                                                            std::size_t hv, float eps,
+                                                            float *__restrict__ conv_state,
+                                                            std::size_t tokens) {
   const std::size_t t = blockIdx.x;
   const std::size_t hidden = hv * kChunkDim;
+  // the convolution history update of the whole call, spread over the grid
+  if (conv_state != nullptr)
+    shift_conv_history<3>(input, conv_state, tokens, stride, conv_dim, t * 256 + threadIdx.x,
+                          tokens * 256);
   for (std::size_t base = 0; base < hidden; base += 2048) {
     const std::size_t c = base + 8 * threadIdx.x;
     const float4 r0 = *reinterpret_cast<const float4 *>(raw + t * hidden + c);
@@ -543,6 +678,117 @@ __global__ __launch_bounds__(256) void recurrent_128_kernel(
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) *reinterpret_cast<float4 *>(sh + (4 * rg + i) * kDim + c0) = s[i];
+}
+
+// Recurrence + output norm for the Qwen3.5 shape (dk = dv = 128) when the
+// whole call is recurrent (decode, short prefill): one workgroup of 8 waves
+// per value head holds the head's full fp32 state, thread (row group rg =
+// tid / 32, column quad cq = tid % 32) rows 8 rg .. 8 rg + 7 of columns
+// 4 cq .. 4 cq + 3, so each state load or store instruction of a wave covers
+// two whole 512-byte rows.  Owning all 128 columns lets the workgroup finish
+// RMSNorm(o) * w * SiLU(z) itself (cpp/kernels/qwen35_delta.cu:578-621), so
+// no separate norm kernel runs.  Same update order as recurrent_128_kernel.
+template <typename T, typename Wt>
+__global__ __launch_bounds__(512) void recurrent_head_norm_kernel(
+    Src<float> qs, Src<float> ks, Src<float> vs, const float *__restrict__ beta,
+    const float *__restrict__ gdecay, float *__restrict__ state, const T *__restrict__ input,
+    const Wt *__restrict__ norm_w, T *__restrict__ output, std::size_t tokens, std::size_t hk,
+    std::size_t hv, std::size_t stride, std::size_t conv_dim, float eps,
+    float *__restrict__ conv_state) {
+  constexpr int kDim = 128, kRows = 8;
+  // the convolution history update of the whole call (multi-token calls),
+  // spread over the grid
+  if (conv_state != nullptr)
+    shift_conv_history<3>(input, conv_state, tokens, stride, conv_dim,
+                          blockIdx.x * 512 + threadIdx.x, hv * 512);
+  __shared__ float4 red[2][8][32]; // [kv / o][wave][column quad]
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int cq = tid & 31, rg = tid >> 5;
+  const std::size_t h = blockIdx.x;
+  const std::size_t kh = h % hk;
+  const int c0 = 4 * cq, r0 = kRows * rg;
+  float *sh = state + h * kDim * kDim;
+  float4 s[kRows];
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) s[i] = *reinterpret_cast<const float4 *>(sh + (r0 + i) * kDim + c0);
+  // norm weight and, per token, the z gate of this lane's four columns
+  float nw[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) nw[i] = Elem<Wt>::load(norm_w, c0 + i);
+  auto row_sum = [&](float4 x, int which) {
+    // lane ^ 32 holds the other row group of this wave for the same quad
+    x.x = sum_xor32(x.x);
+    x.y = sum_xor32(x.y);
+    x.z = sum_xor32(x.z);
+    x.w = sum_xor32(x.w);
+    if (lane < 32) red[which][wave][cq] = x;
+    __syncthreads();
+    float4 t = red[which][0][cq];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) {
+      const float4 u = red[which][w][cq];
+      t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+    }
+    return t;
+  };
+  const std::size_t hidden = hv * kDim;
+  for (std::size_t t = 0; t < tokens; ++t) {
+    const float b = beta[t * hv + h];
+    const float decay = __expf(gdecay[t * hv + h]);
+    float kr[kRows], qr[kRows], vv[4], z[4];
+    const float4 *kp = reinterpret_cast<const float4 *>(ks.base + t * ks.row + kh * ks.head_stride + r0);
+    const float4 *qp = reinterpret_cast<const float4 *>(qs.base + t * qs.row + kh * qs.head_stride + r0);
+#pragma unroll
+    for (int j = 0; j < kRows / 4; ++j) {
+      const float4 a = kp[j], q4 = qp[j];
+      kr[4 * j] = a.x; kr[4 * j + 1] = a.y; kr[4 * j + 2] = a.z; kr[4 * j + 3] = a.w;
+      qr[4 * j] = q4.x; qr[4 * j + 1] = q4.y; qr[4 * j + 2] = q4.z; qr[4 * j + 3] = q4.w;
+    }
+    const float4 v4 = *reinterpret_cast<const float4 *>(vs.base + t * vs.row + h * vs.head_stride + c0);
+    vv[0] = v4.x; vv[1] = v4.y; vv[2] = v4.z; vv[3] = v4.w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      z[i] = Elem<T>::load(input, t * stride + conv_dim + 2 * hv + h * kDim + c0 + i);
+    float4 part = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+      s[i].x *= decay; s[i].y *= decay; s[i].z *= decay; s[i].w *= decay;
+      part.x = fmaf(s[i].x, kr[i], part.x);
+      part.y = fmaf(s[i].y, kr[i], part.y);
+      part.z = fmaf(s[i].z, kr[i], part.z);
+      part.w = fmaf(s[i].w, kr[i], part.w);
+    }
+    const float4 kv = row_sum(part, 0);
+    const float4 d = make_float4((vv[0] - kv.x) * b, (vv[1] - kv.y) * b, (vv[2] - kv.z) * b,
+                                 (vv[3] - kv.w) * b);
+    float4 po = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+      s[i].x = fmaf(kr[i], d.x, s[i].x);
+      s[i].y = fmaf(kr[i], d.y, s[i].y);
+      s[i].z = fmaf(kr[i], d.z, s[i].z);
+      s[i].w = fmaf(kr[i], d.w, s[i].w);
+      po.x = fmaf(s[i].x, qr[i], po.x);
+      po.y = fmaf(s[i].y, qr[i], po.y);
+      po.z = fmaf(s[i].z, qr[i], po.z);
+      po.w = fmaf(s[i].w, qr[i], po.w);
+    }
+    const float4 o = row_sum(po, 1);
+    if (wave == 0) {
+      // lanes 0..31 cover the 32 column quads (lanes 32..63 repeat them)
+      float ss = o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w;
+      ss = sum_xor16(row16_sum(ss));
+      const float scale = rsqrtf(ss / static_cast<float>(kDim) + eps);
+      if (lane < 32) {
+        const std::size_t base = t * hidden + h * kDim + c0;
+        const float ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Elem<T>::store(output, base + i, ov[i] * scale * nw[i] * silu(z[i]));
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) *reinterpret_cast<float4 *>(sh + (r0 + i) * kDim + c0) = s[i];
 }
 
 // ------------------------------------------------- stage 2b: chunked
@@ -1534,7 +1780,27 @@ void launch_typed(const void *input, const void *conv_weight, const void *recurr
                     c.token_stride % 8 == 0 &&
                     (reinterpret_cast<std::uintptr_t>(input) & 15u) == 0 &&
                     (reinterpret_cast<std::uintptr_t>(ws) & 15u) == 0;
-  if (fast) {
+  // The channel-spread convolution also reads weights and history as vectors.
+  const bool wide = fast && ((reinterpret_cast<std::uintptr_t>(conv_weight) |
+                              reinterpret_cast<std::uintptr_t>(conv_state)) & 15u) == 0;
+  const bool chunked = use_chunked(s, policy) && (reinterpret_cast<std::uintptr_t>(ws) & 15u) == 0;
+  const bool one_token_state = wide && s.tokens == 1;
+  constexpr int kConvTokens = 4; // tokens per workgroup of the multi-token convolution
+  if (wide) {
+    const unsigned blocks_y = static_cast<unsigned>(c.conv_dim / kConvWideChannels);
+    if (one_token_state)
+      conv_norm_wide_kernel<T, Wt, 4, 1, true><<<dim3(1, blocks_y, 1), 64, 0, stream>>>(
+          in, static_cast<const Wt *>(conv_weight), conv_state, static_cast<const Wt *>(recurrent_a),
+          static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, s.tokens, c.token_stride,
+          c.conv_dim, 2 * c.key_size, s.value_heads);
+    else
+      conv_norm_wide_kernel<T, Wt, 4, kConvTokens, false>
+          <<<dim3(static_cast<unsigned>(ceil_div_unchecked(s.tokens, kConvTokens)), blocks_y, 1), 64, 0,
+             stream>>>(
+              in, static_cast<const Wt *>(conv_weight), conv_state, static_cast<const Wt *>(recurrent_a),
+              static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, s.tokens, c.token_stride,
+              c.conv_dim, 2 * c.key_size, s.value_heads);
+  } else if (fast) {
     conv_norm_fast_kernel<T, Wt, 4><<<static_cast<unsigned>(s.tokens), 256, 0, stream>>>(
         in, static_cast<const Wt *>(conv_weight), conv_state, static_cast<const Wt *>(recurrent_a),
         static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, c.token_stride, c.conv_dim,
@@ -1547,7 +1813,9 @@ void launch_typed(const void *input, const void *conv_weight, const void *recurr
         s.key_heads, s.value_heads, s.key_dim, s.value_dim, s.conv_width);
   }
   check_launch<Err>("qwen35_gated_delta batched convolution");
-  if (s.conv_width > 1) {
+  // The wide path shifts the history inside its last kernel (the one-token
+  // convolution already did).
+  if (s.conv_width > 1 && !wide) {
     conv_state_kernel<T><<<static_cast<unsigned>(ceil_div_unchecked(c.conv_dim, 256)), 256, 0, stream>>>(
         in, conv_state, s.tokens, c.token_stride, c.conv_dim, s.conv_width);
     check_launch<Err>("qwen35_gated_delta convolution state update");
@@ -1555,15 +1823,23 @@ void launch_typed(const void *input, const void *conv_weight, const void *recurr
   const Src<float> q{convolved, c.conv_dim, s.key_dim, 1.0f};
   const Src<float> k{convolved + c.key_size, c.conv_dim, s.key_dim, 1.0f};
   const Src<float> v{convolved + 2 * c.key_size, c.conv_dim, s.value_dim, 1.0f};
+  if (fast && !chunked && (reinterpret_cast<std::uintptr_t>(rec_state) & 15u) == 0) {
+    // recurrence and output norm in one kernel (one workgroup per value head)
+    recurrent_head_norm_kernel<T, Wt><<<static_cast<unsigned>(s.value_heads), 512, 0, stream>>>(
+        q, k, v, beta, gdecay, rec_state, in, static_cast<const Wt *>(norm_w),
+        static_cast<T *>(output), s.tokens, s.key_heads, s.value_heads, c.token_stride, c.conv_dim,
+        s.epsilon, wide && !one_token_state ? conv_state : nullptr);
+    check_launch<Err>("qwen35_gated_delta register recurrent update");
+    return;
+  }
   launch_recurrence<float, float>(q, k, v, beta, gdecay, rec_state, raw, scratch, s.tokens,
-                                  s.key_heads, s.value_heads, s.key_dim, s.value_dim,
-                                  use_chunked(s, policy) &&
-                                      (reinterpret_cast<std::uintptr_t>(ws) & 15u) == 0,
+                                  s.key_heads, s.value_heads, s.key_dim, s.value_dim, chunked,
                                   stream);
   if (fast)
     out_norm_fast_kernel<T, Wt><<<static_cast<unsigned>(s.tokens), 256, 0, stream>>>(
         in, static_cast<const Wt *>(norm_w), raw, static_cast<T *>(output), c.token_stride,
-        c.conv_dim, s.value_heads, s.epsilon);
+        c.conv_dim, s.value_heads, s.epsilon, wide && !one_token_state ? conv_state : nullptr,
+        s.tokens);
   else
     out_norm_kernel<T, Wt><<<static_cast<unsigned>(s.tokens * s.value_heads), 256, 0, stream>>>(
         in, static_cast<const Wt *>(norm_w), raw, static_cast<T *>(output), c.token_stride, c.conv_dim,

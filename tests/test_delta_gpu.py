@@ -122,7 +122,7 @@ def model_shape(T):
     return dict(tokens=T, hidden=4096, hk=16, hv=32, dk=128, dv=128, width=4, eps=1e-6)
 
 
-@pytest.mark.parametrize("T,schedule", [(3, 0), (1, 2), (17, 1), (128, 0), (150, 0)])
+@pytest.mark.parametrize("T,schedule", [(3, 0), (2, 0), (1, 2), (1, 0), (17, 1), (128, 0), (150, 0)])
 def test_model_shape_schedules(gpu, T, schedule):
     # cpp/tests/qwen35_cuda_delta_test.cu:631-650 plus both gfx950 schedules.
     sh = model_shape(T)
