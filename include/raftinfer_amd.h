@@ -208,6 +208,30 @@ int raftinfer_amd_online_attention_prefill_kernel_only(
  * whose length is 0 or above the maximum context.  Synchronizes the device. */
 int raftinfer_amd_consume_capacity_errors(uint32_t *out);
 
+/* ---- decode graphs (include/raftinfer_amd/hip_graph_decode.hpp) ---- */
+/* Buffers of one decode-attention step (qwen35_executor.cu:2027-2057). */
+typedef struct raftinfer_amd_decode_buffers {
+  const void *query, *key, *value, *gate;
+  void *output, *kv_cache;
+  size_t kv_cache_bytes;
+  void *workspace;
+  size_t workspace_bytes;
+  const uint32_t *device_position;
+} raftinfer_amd_decode_buffers;
+/* Captures one decode-attention graph per context-bucket plan, as
+ * qwen35_executor.cu:2191-2226 builds its variants (CudaGraphDecode,
+ * cuda_graph_decode.cu:20-61, on hipGraph).  Writes an opaque handle. */
+int raftinfer_amd_decode_graphs_create(int device_id, void *stream,
+                                       raftinfer_amd_attention_shape shape, uint8_t mode,
+                                       int activation_dtype, uint8_t cache_dtype,
+                                       uint8_t cache_layout, raftinfer_amd_decode_buffers buffers,
+                                       void **out_handle);
+int raftinfer_amd_decode_graphs_variant_count(void *handle, size_t *out);
+int raftinfer_amd_decode_graphs_variant_for(void *handle, size_t position, size_t *out);
+/* Replays the step of `position`; *device_position must already equal it on the stream. */
+int raftinfer_amd_decode_graphs_replay(void *handle, size_t position);
+void raftinfer_amd_decode_graphs_destroy(void *handle);
+
 /* qwen35_delta.cuh:96-102 (qwen35_gated_delta with a policy). */
 int raftinfer_amd_gated_delta(const void *input, const void *conv_weight, const void *recurrent_a,
                               const void *dt_bias, const void *output_norm_weight, void *output,

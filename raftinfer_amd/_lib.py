@@ -68,6 +68,12 @@ class QkNormRopeShape(ctypes.Structure):
                 ("position_offset", _sz), ("rope_base", ctypes.c_float)]
 
 
+class DecodeBuffers(ctypes.Structure):
+    _fields_ = [("query", _vp), ("key", _vp), ("value", _vp), ("gate", _vp), ("output", _vp),
+                ("kv_cache", _vp), ("kv_cache_bytes", _sz), ("workspace", _vp),
+                ("workspace_bytes", _sz), ("device_position", ctypes.POINTER(ctypes.c_uint32))]
+
+
 # Every symbol include/raftinfer_amd.h declares, with its argument types.
 _I, _F = ctypes.c_int, ctypes.c_float
 _PF = ctypes.POINTER(ctypes.c_float)
@@ -105,6 +111,12 @@ SIGNATURES = {
     "raftinfer_amd_online_attention_prefill_kernel_only":
         ([_vp] * 6 + [_sz, AttentionShape, _I, _u8, _u8, _vp], _I),
     "raftinfer_amd_consume_capacity_errors": ([_PU32], _I),
+    "raftinfer_amd_decode_graphs_create":
+        ([_I, _vp, AttentionShape, _u8, _I, _u8, _u8, DecodeBuffers, ctypes.POINTER(_vp)], _I),
+    "raftinfer_amd_decode_graphs_variant_count": ([_vp, _PSZ], _I),
+    "raftinfer_amd_decode_graphs_variant_for": ([_vp, _sz, _PSZ], _I),
+    "raftinfer_amd_decode_graphs_replay": ([_vp, _sz], _I),
+    "raftinfer_amd_decode_graphs_destroy": ([_vp], None),
     "raftinfer_amd_gated_delta":
         ([_vp] * 6 + [_PF, _PF, _vp, _sz, DeltaShape, DeltaPolicy, _I, _I, _vp], _I),
     "raftinfer_amd_gated_delta_auto":

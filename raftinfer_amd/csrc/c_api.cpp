@@ -4,6 +4,7 @@
 // convention of the reference's cpp/src/c_api.cpp:44, :173-175).
 #include "raftinfer_amd.h"
 
+#include "raftinfer_amd/hip_graph_decode.hpp"
 #include "raftinfer_amd/qwen35_delta.hpp"
 #include "raftinfer_amd/qwen35_online_attention.hpp"
 #include "raftinfer_amd/qwen35_primitives.hpp"
@@ -252,6 +253,47 @@ int raftinfer_amd_online_attention_prefill_kernel_only(
         static_cast<Qwen35KvCacheDType>(cache_dtype), static_cast<Qwen35KvCacheLayout>(cache_layout),
         to_stream(stream));
   });
+}
+
+int raftinfer_amd_decode_graphs_create(int device_id, void *stream,
+                                       raftinfer_amd_attention_shape shape, uint8_t mode, int act,
+                                       uint8_t cache_dtype, uint8_t cache_layout,
+                                       raftinfer_amd_decode_buffers b, void **out_handle) {
+  return guarded([&] {
+    auto &handle = out_ref(out_handle);
+    handle = new Qwen35DecodeAttentionGraphs(
+        device_id, to_stream(stream), to_shape(shape), static_cast<Qwen35DecodeAttentionMode>(mode),
+        to_dtype(act), static_cast<Qwen35KvCacheDType>(cache_dtype),
+        static_cast<Qwen35KvCacheLayout>(cache_layout),
+        Qwen35DecodeAttentionBuffers{b.query, b.key, b.value, b.gate, b.output, b.kv_cache,
+                                     b.kv_cache_bytes, b.workspace, b.workspace_bytes,
+                                     b.device_position});
+  });
+}
+
+int raftinfer_amd_decode_graphs_variant_count(void *handle, size_t *out) {
+  return guarded([&] {
+    if (handle == nullptr) throw Qwen35PrimitiveError("decode graph handle is null");
+    out_ref(out) = static_cast<Qwen35DecodeAttentionGraphs *>(handle)->variant_count();
+  });
+}
+
+int raftinfer_amd_decode_graphs_variant_for(void *handle, size_t position, size_t *out) {
+  return guarded([&] {
+    if (handle == nullptr) throw Qwen35PrimitiveError("decode graph handle is null");
+    out_ref(out) = static_cast<Qwen35DecodeAttentionGraphs *>(handle)->variant_for(position);
+  });
+}
+
+int raftinfer_amd_decode_graphs_replay(void *handle, size_t position) {
+  return guarded([&] {
+    if (handle == nullptr) throw Qwen35PrimitiveError("decode graph handle is null");
+    static_cast<Qwen35DecodeAttentionGraphs *>(handle)->replay(position);
+  });
+}
+
+void raftinfer_amd_decode_graphs_destroy(void *handle) {
+  delete static_cast<Qwen35DecodeAttentionGraphs *>(handle);
 }
 
 int raftinfer_amd_consume_capacity_errors(uint32_t *out) {

@@ -262,6 +262,53 @@ def qwen35_online_attention_decode_batched(query, key, value, gate, output, kv_c
         _ptr(workspace), _nbytes(workspace), shape, activation_dtype, _stream(stream)))
 
 
+class Qwen35DecodeAttentionGraphs:
+    """Per-context-bucket captured decode steps (include/raftinfer_amd/hip_graph_decode.hpp),
+    the variant table of cpp/execution/qwen35_executor.cu:2191-2226 on hipGraph.  The
+    tensors must outlive the object; ``device_position`` (int32/uint32, 1 element) is read
+    by the kernels at replay time."""
+
+    def __init__(self, shape, mode, activation_dtype, cache_dtype, cache_layout, query, key, value,
+                 gate, output, kv_cache, workspace, device_position, stream=None, device_id=0):
+        self._lib = _lib.load()
+        self._keep = (query, key, value, gate, output, kv_cache, workspace, device_position)
+        pos = ctypes.cast(device_position.data_ptr(), ctypes.POINTER(ctypes.c_uint32))
+        buf = _lib.DecodeBuffers(_ptr(query), _ptr(key), _ptr(value), _ptr(gate), _ptr(output),
+                                 _ptr(kv_cache), _nbytes(kv_cache), _ptr(workspace),
+                                 _nbytes(workspace), pos)
+        handle = ctypes.c_void_p()
+        _call(Qwen35PrimitiveError, self._lib.raftinfer_amd_decode_graphs_create(
+            device_id, _stream(stream), shape.c(), mode, activation_dtype, cache_dtype, cache_layout,
+            buf, ctypes.byref(handle)))
+        self._handle = handle
+
+    def variant_count(self) -> int:
+        out = ctypes.c_size_t()
+        _call(Qwen35PrimitiveError, self._lib.raftinfer_amd_decode_graphs_variant_count(
+            self._handle, ctypes.byref(out)))
+        return out.value
+
+    def variant_for(self, position: int) -> int:
+        out = ctypes.c_size_t()
+        _call(Qwen35PrimitiveError, self._lib.raftinfer_amd_decode_graphs_variant_for(
+            self._handle, position, ctypes.byref(out)))
+        return out.value
+
+    def replay(self, position: int) -> None:
+        _call(Qwen35PrimitiveError, self._lib.raftinfer_amd_decode_graphs_replay(self._handle, position))
+
+    def close(self) -> None:
+        if self._handle:
+            self._lib.raftinfer_amd_decode_graphs_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def consume_capacity_errors() -> int:
     out = ctypes.c_uint32()
     _call(Qwen35PrimitiveError, _lib.load().raftinfer_amd_consume_capacity_errors(ctypes.byref(out)))

@@ -160,3 +160,40 @@ def test_captured_prefill_and_delta_core_replay(gpu):
         assert torch.equal(cache, want_cache), f"prefill append replay {replay}"
         assert torch.equal(dout, want_dout), f"delta output replay {replay}"
         assert torch.equal(st, want_st), f"delta state replay {replay}"
+
+
+def test_decode_graph_variants_across_bucket_boundaries(gpu):
+    """The per-bucket variant table (cpp/execution/qwen35_executor.cu:2191-2226) captured by
+    the library's HipGraphDecode (cpp/execution/cuda_graph_decode.cu:20-61): one single-block
+    variant below the split threshold, then one per distinct split-K plan.  Replayed across
+    the 256 threshold and the 512 / 1024 bucket edges, each replay against the oracle."""
+    max_ctx = 1100
+    r = rng(3030)
+    keys, vals = bf16(normal(r, max_ctx, HKV, D)), bf16(normal(r, max_ctx, HKV, D))
+    keys[r.random(max_ctx) < 0.01] *= 8.0
+    cache = to_dev(make_cache(keys, vals, 1, max_ctx), torch.bfloat16)
+    q_np, g_np = bf16(normal(r, HQ, D)), bf16(normal(r, HQ, D))
+    q, g = to_dev(q_np, torch.bfloat16), to_dev(g_np, torch.bfloat16)
+    k_in = torch.empty(HKV * D, device="cuda", dtype=torch.bfloat16)
+    v_in = torch.empty(HKV * D, device="cuda", dtype=torch.bfloat16)
+    out = torch.empty(HQ * D, device="cuda", dtype=torch.bfloat16)
+    shape = ops.Qwen35AttentionShape(1, HQ, HKV, D, max_ctx, 0)
+    ws = torch.empty(ops.qwen35_online_decode_workspace_layout(shape, ops.SPLIT_K_256)[4],
+                     device="cuda", dtype=torch.uint8)
+    pos = torch.zeros(1, device="cuda", dtype=torch.int32)
+    graphs = ops.Qwen35DecodeAttentionGraphs(shape, ops.SPLIT_K_256, 3, 1, 1, q, k_in, v_in, g, out,
+                                             cache, ws, pos, stream=gpu)
+    # single-block, then buckets 512 (cap 2), 1024 (cap 4), 1100 (cap 5)
+    assert graphs.variant_count() == 4
+    assert [graphs.variant_for(p) for p in (0, 254, 255, 510, 511, 1022, 1023, 1099)] == \
+        [0, 0, 1, 1, 1, 2, 2, 3]
+    for position in (254, 255, 256, 510, 511, 512, 1022, 1023, 1024, 1099, 100):
+        k_in.copy_(to_dev(keys[position], torch.bfloat16).flatten())
+        v_in.copy_(to_dev(vals[position], torch.bfloat16).flatten())
+        pos.fill_(position)
+        graphs.replay(position)
+        torch.cuda.synchronize()
+        want = orc.attention_core(q_np[None], keys[:position + 1], vals[:position + 1], g_np[None],
+                                  position)[0]
+        assert_bf16_close(from_dev(out).reshape(HQ, D), bf16(want), what=f"graph position {position}")
+    graphs.close()

@@ -201,6 +201,34 @@ def test_split_partials_merge_to_single_pass(ctx, P):
     assert np.all(np.isnan(pm2[:, active:])) and np.all(np.isfinite(pm2[:, :active]))
 
 
+@pytest.mark.parametrize("ctx,P", [(300, 256), (777, 256), (1024, 512)])
+def test_split_partials_representation_brute_force(ctx, P):
+    # Pins the partial representation itself (cpp/kernels/qwen35_online_attention.cu:602-691):
+    # per (head, partition) m is the partition's true max score in natural-log units
+    # (q.k / sqrt(D)), l = sum exp(score - m) and o = sum exp(score - m) v, unnormalised;
+    # a log2 max, a normalised o or a shifted sum would pass the merge invariant above but
+    # fails here.  float64 brute force, GQA head h reads KV head h // 4.
+    r = rng(ctx + P)
+    hq, hkv, d = 16, 4, 256
+    q = normal(r, hq, d)
+    keys, values = normal(r, ctx, hkv, d), normal(r, ctx, hkv, d)
+    keys[r.random(ctx) < 0.02] *= 8
+    maxp = -(-1025 // P)
+    pm, ps, pv = orc.decode_partials(q, keys, values, ctx, P, maxp)
+    pm, ps, pv = pm.reshape(hq, maxp), ps.reshape(hq, maxp), pv.reshape(hq, maxp, d)
+    for h in range(hq):
+        kv = h // (hq // hkv)
+        for p in range(-(-ctx // P)):
+            k = keys[p * P:min(ctx, (p + 1) * P), kv].astype(np.float64)
+            v = values[p * P:min(ctx, (p + 1) * P), kv].astype(np.float64)
+            sc = k @ q[h].astype(np.float64) / np.sqrt(d)
+            m = sc.max()
+            w = np.exp(sc - m)
+            assert abs(pm[h, p] - m) <= 1e-5 * max(1.0, abs(m))
+            np.testing.assert_allclose(ps[h, p], w.sum(), rtol=1e-5)
+            np.testing.assert_allclose(pv[h, p], w @ v, rtol=1e-4, atol=1e-4)
+
+
 def test_decode_plan_table_matches_reference_test():
     t = KAT["decode_plan_table"]
     shape = tuple(t["shape"])
