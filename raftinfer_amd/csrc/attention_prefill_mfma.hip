@@ -118,10 +118,17 @@ __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(
 // ([tokens][4][256]); the workgroup also writes its own tokens' rows into the
 // cache (the append), so no separate append kernel runs.  Otherwise keys are
 // read from the cache, which already holds them.
+//
+// key_in, value_in and gate are deliberately not __restrict__: the plain append
+// and gate loads must stay where they are issued, between the LDS-direct
+// loads whose hand-written vmcnt waits count them.  With __restrict__ the
+// compiler may sink them past the asm loads (it knows the asm cannot reach
+// restrict-only memory), and the waits would then release K/V tiles that have
+// not landed.
 template <bool HeadMajor, bool FromInput>
 __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
-    const bf16_bits *__restrict__ query, const bf16_bits *__restrict__ key_in,
-    const bf16_bits *__restrict__ value_in, const bf16_bits *__restrict__ gate,
+    const bf16_bits *__restrict__ query, const bf16_bits *key_in,
+    const bf16_bits *value_in, const bf16_bits *gate,
     bf16_bits *__restrict__ output, bf16_bits *__restrict__ cache, std::size_t tokens,
     std::size_t max_ctx, std::size_t past) {
   constexpr bool head_major = HeadMajor;
