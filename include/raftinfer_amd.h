@@ -247,6 +247,18 @@ int raftinfer_amd_gated_delta_auto(const void *input, const void *conv_weight,
                                    void *workspace, size_t workspace_bytes,
                                    raftinfer_amd_delta_shape shape, int dtype, int weight_dtype,
                                    void *stream);
+/* Additive: qwen35_pack_linear_delta_input (qwen35_primitives.cu:388-420)
+ * fused into qwen35_gated_delta; the four projection outputs are read in place
+ * (see qwen35_delta.hpp). */
+int raftinfer_amd_gated_delta_unpacked(const void *qkv, const void *beta, const void *alpha,
+                                       const void *gate, const void *conv_weight,
+                                       const void *recurrent_a, const void *dt_bias,
+                                       const void *output_norm_weight, void *output,
+                                       float *convolution_state, float *recurrent_state,
+                                       void *workspace, size_t workspace_bytes,
+                                       raftinfer_amd_delta_shape shape,
+                                       raftinfer_amd_delta_policy policy, int dtype,
+                                       int weight_dtype, void *stream);
 /* Additive: the recurrence alone; see qwen35_delta.hpp. */
 int raftinfer_amd_gated_delta_core_workspace_bytes(raftinfer_amd_delta_core_shape shape,
                                                    size_t *out);

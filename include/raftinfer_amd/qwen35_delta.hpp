@@ -84,6 +84,23 @@ void qwen35_gated_delta(const void *input, const void *conv_weight, const void *
                         GatedDeltaLaunchPolicy policy, RaftInferDataType dtype,
                         RaftInferDataType weight_dtype, hipStream_t stream);
 
+// ---- Additive: the delta input pack fused into the layer (no counterpart in
+// the reference). ----
+// The same computation as qwen35_pack_linear_delta_input
+// (cpp/kernels/qwen35_primitives.cu:388-420) followed by qwen35_gated_delta,
+// without the packed copy: the kernels read the four projection outputs in
+// place.  qkv: [tokens][2 * key_heads * key_dim + value_heads * value_dim],
+// beta and alpha: [tokens][value_heads], gate: [tokens][hidden_size], all in
+// the activation dtype.  Workspace, states, policy, errors and alignment rules
+// are qwen35_gated_delta's, with the four pointers checked in place of input.
+void qwen35_gated_delta_unpacked(const void *qkv, const void *beta, const void *alpha,
+                                 const void *gate, const void *conv_weight, const void *recurrent_a,
+                                 const void *dt_bias, const void *output_norm_weight, void *output,
+                                 float *convolution_state, float *recurrent_state, void *workspace,
+                                 std::size_t workspace_bytes, GatedDeltaShape shape,
+                                 GatedDeltaLaunchPolicy policy, RaftInferDataType dtype,
+                                 RaftInferDataType weight_dtype, hipStream_t stream);
+
 // ---- Additive: the recurrence alone (no counterpart in the reference). ----
 // q, k: bf16 [tokens][key_heads][key_dim] (already L2-normalised; q is
 // multiplied by q_scale), v: bf16 [tokens][value_heads][value_dim],

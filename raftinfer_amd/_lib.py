@@ -121,6 +121,8 @@ SIGNATURES = {
         ([_vp] * 6 + [_PF, _PF, _vp, _sz, DeltaShape, DeltaPolicy, _I, _I, _vp], _I),
     "raftinfer_amd_gated_delta_auto":
         ([_vp] * 6 + [_PF, _PF, _vp, _sz, DeltaShape, _I, _I, _vp], _I),
+    "raftinfer_amd_gated_delta_unpacked":
+        ([_vp] * 9 + [_PF, _PF, _vp, _sz, DeltaShape, DeltaPolicy, _I, _I, _vp], _I),
     "raftinfer_amd_gated_delta_core_workspace_bytes": ([DeltaCoreShape, _PSZ], _I),
     "raftinfer_amd_gated_delta_core":
         ([_vp, _vp, _vp, _PF, _PF, _F, _PF, _vp, _vp, _sz, DeltaCoreShape, _I, _vp], _I),

@@ -324,6 +324,22 @@ int raftinfer_amd_gated_delta_auto(const void *input, const void *conv_weight, c
   });
 }
 
+int raftinfer_amd_gated_delta_unpacked(const void *qkv, const void *beta, const void *alpha,
+                                       const void *gate, const void *conv_weight,
+                                       const void *recurrent_a, const void *dt_bias,
+                                       const void *norm_w, void *output, float *conv_state,
+                                       float *rec_state, void *workspace, size_t workspace_bytes,
+                                       raftinfer_amd_delta_shape shape,
+                                       raftinfer_amd_delta_policy policy, int dtype,
+                                       int weight_dtype, void *stream) {
+  return guarded([&] {
+    qwen35_gated_delta_unpacked(qkv, beta, alpha, gate, conv_weight, recurrent_a, dt_bias, norm_w,
+                                output, conv_state, rec_state, workspace, workspace_bytes,
+                                to_delta(shape), to_delta_policy(policy), to_dtype(dtype),
+                                to_dtype(weight_dtype), to_stream(stream));
+  });
+}
+
 int raftinfer_amd_gated_delta_core_workspace_bytes(raftinfer_amd_delta_core_shape s, size_t *out) {
   return guarded([&] {
     out_ref(out) = qwen35_gated_delta_core_workspace_bytes(

@@ -199,14 +199,36 @@ template <typename T> struct OutRows {
   __device__ __forceinline__ void put(std::size_t idx, float v) const { Elem<T>::store(base, idx, v); }
 };
 
+// Where a token's input rows come from: the packed [q k v | b | a | z] row of
+// qwen35_gated_delta (cpp/kernels/qwen35_delta.cuh:77-86; every stride is the
+// packed width), or the four projection outputs that
+// qwen35_pack_linear_delta_input would pack (cpp/kernels/qwen35_primitives.cu:
+// 388-420), read in place by qwen35_gated_delta_unpacked.
+template <typename T> struct DeltaRows {
+  const T *qkv; // conv channel c of token t at qkv[t * qkv_stride + c]
+  std::size_t qkv_stride;
+  const T *b; // beta logit of value head h at b[t * b_stride + h]
+  std::size_t b_stride;
+  const T *a; // decay logit
+  std::size_t a_stride;
+  const T *z; // output gate, value channel c at z[t * z_stride + c]
+  std::size_t z_stride;
+  __device__ __forceinline__ float x(std::size_t t, std::size_t c) const {
+    return Elem<T>::load(qkv, t * qkv_stride + c);
+  }
+  __device__ __forceinline__ float gate(std::size_t t, std::size_t c) const {
+    return Elem<T>::load(z, t * z_stride + c);
+  }
+};
+
 // -------------------------------------------------------- stage 1 kernels
 
 // Block (token, vector): vector < Hk -> q head, < 2Hk -> k head, else v head.
 template <typename T, typename Wt>
 __global__ __launch_bounds__(256) void conv_norm_kernel(
-    const T *__restrict__ input, const Wt *__restrict__ conv_w, const float *__restrict__ conv_state,
+    DeltaRows<T> in, const Wt *__restrict__ conv_w, const float *__restrict__ conv_state,
     const Wt *__restrict__ recurrent_a, const Wt *__restrict__ dt_bias, float *__restrict__ convolved,
-    float *__restrict__ beta, float *__restrict__ gdecay, std::size_t tokens, std::size_t stride,
+    float *__restrict__ beta, float *__restrict__ gdecay, std::size_t tokens,
     std::size_t conv_dim, std::size_t hk, std::size_t hv, std::size_t dk, std::size_t dv,
     std::size_t width) {
   __shared__ float red[4];
@@ -222,11 +244,11 @@ __global__ __launch_bounds__(256) void conv_norm_kernel(
   for (std::size_t i = threadIdx.x; i < len; i += 256, ++n) {
     const std::size_t ch = base + i;
     const std::size_t wb = ch * width;
-    float sum = Elem<T>::load(input, t * stride + ch) * Elem<Wt>::load(conv_w, wb + hist);
+    float sum = in.x(t, ch) * Elem<Wt>::load(conv_w, wb + hist);
     for (std::size_t h = 0; h < hist; ++h) {
       const std::size_t src = t + h;
       const float prev = src < hist ? conv_state[ch * hist + src]
-                                    : Elem<T>::load(input, (src - hist) * stride + ch);
+                                    : in.x(src - hist, ch);
       sum += prev * Elem<Wt>::load(conv_w, wb + h);
     }
     const float y = silu(sum);
@@ -247,11 +269,11 @@ __global__ __launch_bounds__(256) void conv_norm_kernel(
       if (n >= 4) { // dims > 1024: recompute (never hit for Qwen3.5 shapes)
         const std::size_t ch = base + i;
         const std::size_t wb = ch * width;
-        float sum = Elem<T>::load(input, t * stride + ch) * Elem<Wt>::load(conv_w, wb + hist);
+        float sum = in.x(t, ch) * Elem<Wt>::load(conv_w, wb + hist);
         for (std::size_t h = 0; h < hist; ++h) {
           const std::size_t src = t + h;
           const float prev = src < hist ? conv_state[ch * hist + src]
-                                        : Elem<T>::load(input, (src - hist) * stride + ch);
+                                        : in.x(src - hist, ch);
           sum += prev * Elem<Wt>::load(conv_w, wb + h);
         }
         y = silu(sum);
@@ -261,8 +283,8 @@ __global__ __launch_bounds__(256) void conv_norm_kernel(
   }
   if (vec == 0) {
     for (std::size_t h = threadIdx.x; h < hv; h += 256) {
-      const float b = Elem<T>::load(input, t * stride + conv_dim + h);
-      const float a = Elem<T>::load(input, t * stride + conv_dim + hv + h);
+      const float b = Elem<T>::load(in.b, t * in.b_stride + h);
+      const float a = Elem<T>::load(in.a, t * in.a_stride + h);
       beta[t * hv + h] = sigmoid(b);
       gdecay[t * hv + h] = Elem<Wt>::load(recurrent_a, h) * softplus(a + Elem<Wt>::load(dt_bias, h));
     }
@@ -292,9 +314,9 @@ template <typename T> __device__ __forceinline__ void load8(const T *p, float (&
 // reduce in-row.  Same math as conv_norm_kernel.
 template <typename T, typename Wt, int W>
 __global__ __launch_bounds__(256) void conv_norm_fast_kernel(
-    const T *__restrict__ input, const Wt *__restrict__ conv_w, const float *__restrict__ conv_state,
+    DeltaRows<T> in, const Wt *__restrict__ conv_w, const float *__restrict__ conv_state,
     const Wt *__restrict__ recurrent_a, const Wt *__restrict__ dt_bias, float *__restrict__ convolved,
-    float *__restrict__ beta, float *__restrict__ gdecay, std::size_t stride, std::size_t conv_dim,
+    float *__restrict__ beta, float *__restrict__ gdecay, std::size_t conv_dim,
     std::size_t qk_channels, std::size_t hv) {
   constexpr int H = W - 1;
   const std::size_t t = blockIdx.x;
@@ -302,7 +324,7 @@ __global__ __launch_bounds__(256) void conv_norm_fast_kernel(
   for (std::size_t base = 0; base < conv_dim; base += 2048) {
     const std::size_t c = base + 8 * threadIdx.x;
     float cur[8], prev[H > 0 ? H : 1][8], w[8][W];
-    load8(input + t * stride + c, cur);
+    load8(in.qkv + t * in.qkv_stride + c, cur);
 #pragma unroll
     for (int h = 0; h < H; ++h) {
       const std::size_t src = t + h;
@@ -310,7 +332,7 @@ __global__ __launch_bounds__(256) void conv_norm_fast_kernel(
 #pragma unroll
         for (int e = 0; e < 8; ++e) prev[h][e] = conv_state[(c + e) * H + src];
       } else {
-        load8(input + (src - H) * stride + c, prev[h]);
+        load8(in.qkv + (src - H) * in.qkv_stride + c, prev[h]);
       }
     }
 #pragma unroll
@@ -338,8 +360,8 @@ __global__ __launch_bounds__(256) void conv_norm_fast_kernel(
     *reinterpret_cast<float4 *>(dst + 4) = make_float4(y[4], y[5], y[6], y[7]);
   }
   for (std::size_t h = threadIdx.x; h < hv; h += 256) {
-    const float b = Elem<T>::load(input, t * stride + conv_dim + h);
-    const float a = Elem<T>::load(input, t * stride + conv_dim + hv + h);
+    const float b = Elem<T>::load(in.b, t * in.b_stride + h);
+    const float a = Elem<T>::load(in.a, t * in.a_stride + h);
     beta[t * hv + h] = sigmoid(b);
     gdecay[t * hv + h] = Elem<Wt>::load(recurrent_a, h) * softplus(a + Elem<Wt>::load(dt_bias, h));
   }
@@ -357,9 +379,9 @@ __global__ __launch_bounds__(256) void conv_norm_fast_kernel(
 constexpr int kConvWideChannels = 512;
 template <typename T, typename Wt, int W, int TT, bool kUpdateState>
 __global__ __launch_bounds__(64) void conv_norm_wide_kernel(
-    const T *__restrict__ input, const Wt *__restrict__ conv_w, float *__restrict__ conv_state,
+    DeltaRows<T> in, const Wt *__restrict__ conv_w, float *__restrict__ conv_state,
     const Wt *__restrict__ recurrent_a, const Wt *__restrict__ dt_bias, float *__restrict__ convolved,
-    float *__restrict__ beta, float *__restrict__ gdecay, std::size_t tokens, std::size_t stride,
+    float *__restrict__ beta, float *__restrict__ gdecay, std::size_t tokens,
     std::size_t conv_dim, std::size_t qk_channels, std::size_t hv) {
   constexpr int H = W - 1;
   static_assert(H == 3, "history vectors assume a width-4 convolution");
@@ -372,7 +394,7 @@ __global__ __launch_bounds__(64) void conv_norm_wide_kernel(
 #pragma unroll
   for (int u = 0; u < TT; ++u) {
     const std::size_t t = t0 + u < tokens ? t0 + u : tokens - 1;
-    load8(input + t * stride + c, win[H + u]);
+    load8(in.qkv + t * in.qkv_stride + c, win[H + u]);
   }
 #pragma unroll
   for (int j = 0; j < W; ++j) {
@@ -397,7 +419,7 @@ __global__ __launch_bounds__(64) void conv_norm_wide_kernel(
 #pragma unroll
       for (int e = 0; e < 8; ++e) win[h][e] = hist[e * H + static_cast<int>(src)];
     } else {
-      load8(input + (src - H) * stride + c, win[h]);
+      load8(in.qkv + (src - H) * in.qkv_stride + c, win[h]);
     }
   }
   const bool qk = c < qk_channels;
@@ -441,8 +463,8 @@ __global__ __launch_bounds__(64) void conv_norm_wide_kernel(
     for (int i = threadIdx.x; i < TT * static_cast<int>(hv); i += 64) {
       const std::size_t t = t0 + i / hv, h = i % hv;
       if (t >= tokens) break;
-      const float b = Elem<T>::load(input, t * stride + conv_dim + h);
-      const float a = Elem<T>::load(input, t * stride + conv_dim + hv + h);
+      const float b = Elem<T>::load(in.b, t * in.b_stride + h);
+      const float a = Elem<T>::load(in.a, t * in.a_stride + h);
       beta[t * hv + h] = sigmoid(b);
       gdecay[t * hv + h] = Elem<Wt>::load(recurrent_a, h) * softplus(a + Elem<Wt>::load(dt_bias, h));
     }
@@ -456,18 +478,17 @@ __global__ __launch_bounds__(64) void conv_norm_wide_kernel(
 // finished (a later launch on the same stream), and each channel has one
 // owner, so the update is race-free.
 template <int H, typename T>
-__device__ __forceinline__ void shift_conv_history(const T *__restrict__ input,
+__device__ __forceinline__ void shift_conv_history(const DeltaRows<T> &in,
                                                    float *__restrict__ conv_state,
-                                                   std::size_t tokens, std::size_t stride,
-                                                   std::size_t conv_dim, std::size_t first,
-                                                   std::size_t step) {
+                                                   std::size_t tokens, std::size_t conv_dim,
+                                                   std::size_t first, std::size_t step) {
   for (std::size_t ch = first; ch < conv_dim; ch += step) {
     float nh[H];
 #pragma unroll
     for (int s = 0; s < H; ++s) {
       const std::size_t src = tokens + s; // extended index
       nh[s] = src < static_cast<std::size_t>(H) ? conv_state[ch * H + src]
-                                                : Elem<T>::load(input, (src - H) * stride + ch);
+                                                : in.x(src - H, ch);
     }
 #pragma unroll
     for (int s = 0; s < H; ++s) conv_state[ch * H + s] = nh[s];
@@ -476,20 +497,19 @@ __device__ __forceinline__ void shift_conv_history(const T *__restrict__ input,
 
 // One block per token; a 128-wide value head is one 16-lane DPP row.
 template <typename T, typename Wt>
-__global__ __launch_bounds__(256) void out_norm_fast_kernel(const T *__restrict__ input,
+__global__ __launch_bounds__(256) void out_norm_fast_kernel(DeltaRows<T> in,
                                                             const Wt *__restrict__ norm_w,
                                                             const float *__restrict__ raw,
                                                             T *__restrict__ output,
-                                                            std::size_t stride, std::size_t conv_dim,
-                                                            std::size_t hv, float eps,
+                                                            std::size_t conv_dim, std::size_t hv,
+                                                            float eps,
                                                             float *__restrict__ conv_state,
                                                             std::size_t tokens) {
   const std::size_t t = blockIdx.x;
   const std::size_t hidden = hv * kChunkDim;
   // the convolution history update of the whole call, spread over the grid
   if (conv_state != nullptr)
-    shift_conv_history<3>(input, conv_state, tokens, stride, conv_dim, t * 256 + threadIdx.x,
-                          tokens * 256);
+    shift_conv_history<3>(in, conv_state, tokens, conv_dim, t * 256 + threadIdx.x, tokens * 256);
   for (std::size_t base = 0; base < hidden; base += 2048) {
     const std::size_t c = base + 8 * threadIdx.x;
     const float4 r0 = *reinterpret_cast<const float4 *>(raw + t * hidden + c);
@@ -501,7 +521,7 @@ __global__ __launch_bounds__(256) void out_norm_fast_kernel(const T *__restrict_
     ss = row16_sum(ss);
     const float scale = rsqrtf(ss / static_cast<float>(kChunkDim) + eps);
     float z[8];
-    load8(input + t * stride + conv_dim + 2 * hv + c, z);
+    load8(in.z + t * in.z_stride + c, z);
     const std::size_t wc = c % kChunkDim;
 #pragma unroll
     for (int e = 0; e < 8; ++e)
@@ -511,17 +531,17 @@ __global__ __launch_bounds__(256) void out_norm_fast_kernel(const T *__restrict_
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void conv_state_kernel(const T *__restrict__ input,
+__global__ __launch_bounds__(256) void conv_state_kernel(DeltaRows<T> in,
                                                          float *__restrict__ conv_state,
-                                                         std::size_t tokens, std::size_t stride,
-                                                         std::size_t conv_dim, std::size_t width) {
+                                                         std::size_t tokens, std::size_t conv_dim,
+                                                         std::size_t width) {
   const std::size_t ch = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (ch >= conv_dim) return;
   const std::size_t hist = width - 1;
   for (std::size_t h = 0; h < hist; ++h) {
     const std::size_t src = tokens + h;
     conv_state[ch * hist + h] = src < hist ? conv_state[ch * hist + src]
-                                           : Elem<T>::load(input, (src - hist) * stride + ch);
+                                           : in.x(src - hist, ch);
   }
 }
 
@@ -691,16 +711,15 @@ __global__ __launch_bounds__(256) void recurrent_128_kernel(
 template <typename T, typename Wt>
 __global__ __launch_bounds__(512) void recurrent_head_norm_kernel(
     Src<float> qs, Src<float> ks, Src<float> vs, const float *__restrict__ beta,
-    const float *__restrict__ gdecay, float *__restrict__ state, const T *__restrict__ input,
+    const float *__restrict__ gdecay, float *__restrict__ state, DeltaRows<T> in,
     const Wt *__restrict__ norm_w, T *__restrict__ output, std::size_t tokens, std::size_t hk,
-    std::size_t hv, std::size_t stride, std::size_t conv_dim, float eps,
+    std::size_t hv, std::size_t conv_dim, float eps,
     float *__restrict__ conv_state) {
   constexpr int kDim = 128, kRows = 8;
   // the convolution history update of the whole call (multi-token calls),
   // spread over the grid
   if (conv_state != nullptr)
-    shift_conv_history<3>(input, conv_state, tokens, stride, conv_dim,
-                          blockIdx.x * 512 + threadIdx.x, hv * 512);
+    shift_conv_history<3>(in, conv_state, tokens, conv_dim, blockIdx.x * 512 + threadIdx.x, hv * 512);
   __shared__ float4 red[2][8][32]; // [kv / o][wave][column quad]
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int cq = tid & 31, rg = tid >> 5;
@@ -748,7 +767,7 @@ __global__ __launch_bounds__(512) void recurrent_head_norm_kernel(
     vv[0] = v4.x; vv[1] = v4.y; vv[2] = v4.z; vv[3] = v4.w;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      z[i] = Elem<T>::load(input, t * stride + conv_dim + 2 * hv + h * kDim + c0 + i);
+      z[i] = in.gate(t, h * kDim + c0 + i);
     float4 part = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int i = 0; i < kRows; ++i) {
@@ -1690,11 +1709,10 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
 // Block (token, value head): RMSNorm over dv, x weight, x SiLU(z)
 // (cpp/kernels/qwen35_delta.cu:578-621).
 template <typename T, typename Wt>
-__global__ __launch_bounds__(256) void out_norm_kernel(const T *__restrict__ input,
+__global__ __launch_bounds__(256) void out_norm_kernel(DeltaRows<T> in,
                                                        const Wt *__restrict__ norm_w,
                                                        const float *__restrict__ raw,
-                                                       T *__restrict__ output, std::size_t stride,
-                                                       std::size_t conv_dim, std::size_t hv,
+                                                       T *__restrict__ output, std::size_t hv,
                                                        std::size_t dv, float eps) {
   __shared__ float red[4];
   const std::size_t t = blockIdx.x / hv, h = blockIdx.x % hv;
@@ -1706,10 +1724,10 @@ __global__ __launch_bounds__(256) void out_norm_kernel(const T *__restrict__ inp
   __syncthreads();
   const float total = red[0] + red[1] + red[2] + red[3];
   const float scale = rsqrtf(total / static_cast<float>(dv) + eps);
-  const std::size_t zb = t * stride + conv_dim + 2 * hv + h * dv;
+  const std::size_t zb = h * dv;
   for (std::size_t i = threadIdx.x; i < dv; i += 256) {
     const float n = raw[base + i] * scale * Elem<Wt>::load(norm_w, i);
-    Elem<T>::store(output, base + i, n * silu(Elem<T>::load(input, zb + i)));
+    Elem<T>::store(output, base + i, n * silu(in.gate(t, zb + i)));
   }
 }
 
@@ -1751,6 +1769,18 @@ void launch_recurrence(Src<InT> q, Src<InT> k, Src<InT> v, const float *beta, co
   check_launch<Err>("qwen35_gated_delta register recurrent update");
 }
 
+// Host-side, type-erased DeltaRows: base pointers and strides in elements.
+struct DeltaSources {
+  const void *qkv;
+  std::size_t qkv_stride;
+  const void *b;
+  std::size_t b_stride;
+  const void *a;
+  std::size_t a_stride;
+  const void *z;
+  std::size_t z_stride;
+};
+
 bool use_chunked(const GatedDeltaShape &s, const GatedDeltaLaunchPolicy &p) {
   if (s.key_dim != kChunkDim || s.value_dim != kChunkDim) return false;
   if (p.schedule == GatedDeltaSchedule::register_resident_prefill_sm120) return true;
@@ -1759,11 +1789,14 @@ bool use_chunked(const GatedDeltaShape &s, const GatedDeltaLaunchPolicy &p) {
 }
 
 template <typename T, typename Wt>
-void launch_typed(const void *input, const void *conv_weight, const void *recurrent_a,
+void launch_typed(const DeltaSources &src, const void *conv_weight, const void *recurrent_a,
                   const void *dt_bias, const void *norm_w, void *output, float *conv_state,
                   float *rec_state, float *ws, const GatedDeltaShape &s, const CheckedShape &c,
                   const GatedDeltaLaunchPolicy &policy, hipStream_t stream) {
-  const auto *in = static_cast<const T *>(input);
+  const DeltaRows<T> in{static_cast<const T *>(src.qkv), src.qkv_stride,
+                        static_cast<const T *>(src.b),   src.b_stride,
+                        static_cast<const T *>(src.a),   src.a_stride,
+                        static_cast<const T *>(src.z),   src.z_stride};
   float *convolved = ws;
   float *raw = convolved + s.tokens * c.conv_dim;
   float *beta = raw + s.tokens * s.hidden_size;
@@ -1777,9 +1810,9 @@ void launch_typed(const void *input, const void *conv_weight, const void *recurr
 
   const bool fast = s.key_dim == kChunkDim && s.value_dim == kChunkDim && s.conv_width == 4 &&
                     c.conv_dim % 2048 == 0 && s.hidden_size % 2048 == 0 &&
-                    c.token_stride % 8 == 0 &&
-                    (reinterpret_cast<std::uintptr_t>(input) & 15u) == 0 &&
-                    (reinterpret_cast<std::uintptr_t>(ws) & 15u) == 0;
+                    src.qkv_stride % 8 == 0 && src.z_stride % 8 == 0 &&
+                    ((reinterpret_cast<std::uintptr_t>(src.qkv) | reinterpret_cast<std::uintptr_t>(src.z) |
+                      reinterpret_cast<std::uintptr_t>(ws)) & 15u) == 0;
   // The channel-spread convolution also reads weights and history as vectors.
   const bool wide = fast && ((reinterpret_cast<std::uintptr_t>(conv_weight) |
                               reinterpret_cast<std::uintptr_t>(conv_state)) & 15u) == 0;
@@ -1791,25 +1824,25 @@ void launch_typed(const void *input, const void *conv_weight, const void *recurr
     if (one_token_state)
       conv_norm_wide_kernel<T, Wt, 4, 1, true><<<dim3(1, blocks_y, 1), 64, 0, stream>>>(
           in, static_cast<const Wt *>(conv_weight), conv_state, static_cast<const Wt *>(recurrent_a),
-          static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, s.tokens, c.token_stride,
+          static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, s.tokens,
           c.conv_dim, 2 * c.key_size, s.value_heads);
     else
       conv_norm_wide_kernel<T, Wt, 4, kConvTokens, false>
           <<<dim3(static_cast<unsigned>(ceil_div_unchecked(s.tokens, kConvTokens)), blocks_y, 1), 64, 0,
              stream>>>(
               in, static_cast<const Wt *>(conv_weight), conv_state, static_cast<const Wt *>(recurrent_a),
-              static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, s.tokens, c.token_stride,
+              static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, s.tokens,
               c.conv_dim, 2 * c.key_size, s.value_heads);
   } else if (fast) {
     conv_norm_fast_kernel<T, Wt, 4><<<static_cast<unsigned>(s.tokens), 256, 0, stream>>>(
         in, static_cast<const Wt *>(conv_weight), conv_state, static_cast<const Wt *>(recurrent_a),
-        static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, c.token_stride, c.conv_dim,
+        static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, c.conv_dim,
         2 * c.key_size, s.value_heads);
   } else {
     const dim3 cgrid{static_cast<unsigned>(s.tokens), static_cast<unsigned>(2 * s.key_heads + s.value_heads), 1};
     conv_norm_kernel<T, Wt><<<cgrid, 256, 0, stream>>>(
         in, static_cast<const Wt *>(conv_weight), conv_state, static_cast<const Wt *>(recurrent_a),
-        static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, s.tokens, c.token_stride, c.conv_dim,
+        static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, s.tokens, c.conv_dim,
         s.key_heads, s.value_heads, s.key_dim, s.value_dim, s.conv_width);
   }
   check_launch<Err>("qwen35_gated_delta batched convolution");
@@ -1817,7 +1850,7 @@ void launch_typed(const void *input, const void *conv_weight, const void *recurr
   // convolution already did).
   if (s.conv_width > 1 && !wide) {
     conv_state_kernel<T><<<static_cast<unsigned>(ceil_div_unchecked(c.conv_dim, 256)), 256, 0, stream>>>(
-        in, conv_state, s.tokens, c.token_stride, c.conv_dim, s.conv_width);
+        in, conv_state, s.tokens, c.conv_dim, s.conv_width);
     check_launch<Err>("qwen35_gated_delta convolution state update");
   }
   const Src<float> q{convolved, c.conv_dim, s.key_dim, 1.0f};
@@ -1827,7 +1860,7 @@ void launch_typed(const void *input, const void *conv_weight, const void *recurr
     // recurrence and output norm in one kernel (one workgroup per value head)
     recurrent_head_norm_kernel<T, Wt><<<static_cast<unsigned>(s.value_heads), 512, 0, stream>>>(
         q, k, v, beta, gdecay, rec_state, in, static_cast<const Wt *>(norm_w),
-        static_cast<T *>(output), s.tokens, s.key_heads, s.value_heads, c.token_stride, c.conv_dim,
+        static_cast<T *>(output), s.tokens, s.key_heads, s.value_heads, c.conv_dim,
         s.epsilon, wide && !one_token_state ? conv_state : nullptr);
     check_launch<Err>("qwen35_gated_delta register recurrent update");
     return;
@@ -1837,18 +1870,17 @@ void launch_typed(const void *input, const void *conv_weight, const void *recurr
                                   stream);
   if (fast)
     out_norm_fast_kernel<T, Wt><<<static_cast<unsigned>(s.tokens), 256, 0, stream>>>(
-        in, static_cast<const Wt *>(norm_w), raw, static_cast<T *>(output), c.token_stride,
-        c.conv_dim, s.value_heads, s.epsilon, wide && !one_token_state ? conv_state : nullptr,
-        s.tokens);
+        in, static_cast<const Wt *>(norm_w), raw, static_cast<T *>(output), c.conv_dim,
+        s.value_heads, s.epsilon, wide && !one_token_state ? conv_state : nullptr, s.tokens);
   else
     out_norm_kernel<T, Wt><<<static_cast<unsigned>(s.tokens * s.value_heads), 256, 0, stream>>>(
-        in, static_cast<const Wt *>(norm_w), raw, static_cast<T *>(output), c.token_stride, c.conv_dim,
-        s.value_heads, s.value_dim, s.epsilon);
+        in, static_cast<const Wt *>(norm_w), raw, static_cast<T *>(output), s.value_heads,
+        s.value_dim, s.epsilon);
   check_launch<Err>("qwen35_gated_delta batched output normalization");
 }
 
 template <typename T>
-void launch_for_weights(RaftInferDataType wdt, const void *input, const void *conv_weight,
+void launch_for_weights(RaftInferDataType wdt, const DeltaSources &input, const void *conv_weight,
                         const void *recurrent_a, const void *dt_bias, const void *norm_w,
                         void *output, float *conv_state, float *rec_state, float *ws,
                         const GatedDeltaShape &s, const CheckedShape &c,
@@ -1907,18 +1939,23 @@ void qwen35_gated_delta(const void *input, const void *conv_weight, const void *
                      stream);
 }
 
-// Validation order and messages: cpp/kernels/qwen35_delta.cu:811-897.
-void qwen35_gated_delta(const void *input, const void *conv_weight, const void *recurrent_a,
-                        const void *dt_bias, const void *norm_w, void *output, float *conv_state,
-                        float *rec_state, void *workspace, std::size_t workspace_bytes,
-                        GatedDeltaShape shape, GatedDeltaLaunchPolicy policy,
-                        RaftInferDataType dtype, RaftInferDataType weight_dtype,
-                        hipStream_t stream) {
+namespace {
+// Validation of everything but the input rows, in the reference's order
+// (cpp/kernels/qwen35_delta.cu:811-897); `check_inputs` runs where the
+// reference checks its input pointer and its alignment.
+template <typename InputCheck, typename AlignCheck>
+CheckedShape validate_call(InputCheck check_inputs, AlignCheck align_inputs, const void *conv_weight,
+                           const void *recurrent_a, const void *dt_bias, const void *norm_w,
+                           const void *output, const float *conv_state, const float *rec_state,
+                           const void *workspace, std::size_t workspace_bytes,
+                           const GatedDeltaShape &shape, const GatedDeltaLaunchPolicy &policy,
+                           RaftInferDataType dtype, RaftInferDataType weight_dtype,
+                           hipStream_t stream) {
   const CheckedShape c = validate_shape(shape);
   validate_policy(policy, shape);
   require_dtype(dtype);
   require_weight_dtype(dtype, weight_dtype);
-  require<Err>(input != nullptr, "gated-delta input pointer is null");
+  check_inputs();
   require<Err>(conv_weight != nullptr, "gated-delta convolution weight pointer is null");
   require<Err>(recurrent_a != nullptr, "gated-delta recurrent coefficient pointer is null");
   require<Err>(dt_bias != nullptr, "gated-delta dt-bias pointer is null");
@@ -1932,7 +1969,7 @@ void qwen35_gated_delta(const void *input, const void *conv_weight, const void *
   require<Err>(workspace_bytes >= c.workspace_bytes, "gated-delta workspace is too small");
   const std::size_t da = dtype == RAFTINFER_DTYPE_F32 ? 4 : 2;
   const std::size_t wa = weight_dtype == RAFTINFER_DTYPE_F32 ? 4 : 2;
-  require_aligned(input, da, "gated-delta input is not dtype-aligned");
+  align_inputs(da);
   require_aligned(conv_weight, wa, "gated-delta convolution weight is not dtype-aligned");
   require_aligned(recurrent_a, wa, "gated-delta recurrent coefficient is not dtype-aligned");
   require_aligned(dt_bias, wa, "gated-delta dt-bias weight is not dtype-aligned");
@@ -1945,17 +1982,79 @@ void qwen35_gated_delta(const void *input, const void *conv_weight, const void *
   require<Err>(stream != nullptr, "HIP stream is null");
   // Register recurrence keeps at most 32 rows per lane across 8 waves.
   require<Err>(shape.key_dim <= kRecWaves * 32, "gated-delta key_dim above 256 is not supported");
+  return c;
+}
 
+void dispatch(const DeltaSources &src, const void *conv_weight, const void *recurrent_a,
+              const void *dt_bias, const void *norm_w, void *output, float *conv_state,
+              float *rec_state, void *workspace, const GatedDeltaShape &shape, const CheckedShape &c,
+              const GatedDeltaLaunchPolicy &policy, RaftInferDataType dtype,
+              RaftInferDataType weight_dtype, hipStream_t stream) {
   auto *ws = static_cast<float *>(workspace);
   if (dtype == RAFTINFER_DTYPE_F32)
-    launch_for_weights<float>(weight_dtype, input, conv_weight, recurrent_a, dt_bias, norm_w, output,
+    launch_for_weights<float>(weight_dtype, src, conv_weight, recurrent_a, dt_bias, norm_w, output,
                               conv_state, rec_state, ws, shape, c, policy, stream);
   else if (dtype == RAFTINFER_DTYPE_F16)
-    launch_for_weights<_Float16>(weight_dtype, input, conv_weight, recurrent_a, dt_bias, norm_w,
+    launch_for_weights<_Float16>(weight_dtype, src, conv_weight, recurrent_a, dt_bias, norm_w,
                                  output, conv_state, rec_state, ws, shape, c, policy, stream);
   else
-    launch_for_weights<bf16_bits>(weight_dtype, input, conv_weight, recurrent_a, dt_bias, norm_w,
+    launch_for_weights<bf16_bits>(weight_dtype, src, conv_weight, recurrent_a, dt_bias, norm_w,
                                   output, conv_state, rec_state, ws, shape, c, policy, stream);
+}
+} // namespace
+
+// Validation order and messages: cpp/kernels/qwen35_delta.cu:811-897.
+void qwen35_gated_delta(const void *input, const void *conv_weight, const void *recurrent_a,
+                        const void *dt_bias, const void *norm_w, void *output, float *conv_state,
+                        float *rec_state, void *workspace, std::size_t workspace_bytes,
+                        GatedDeltaShape shape, GatedDeltaLaunchPolicy policy,
+                        RaftInferDataType dtype, RaftInferDataType weight_dtype,
+                        hipStream_t stream) {
+  const CheckedShape c = validate_call(
+      [&] { require<Err>(input != nullptr, "gated-delta input pointer is null"); },
+      [&](std::size_t da) { require_aligned(input, da, "gated-delta input is not dtype-aligned"); },
+      conv_weight, recurrent_a, dt_bias, norm_w, output, conv_state, rec_state, workspace,
+      workspace_bytes, shape, policy, dtype, weight_dtype, stream);
+  // The packed row [q k v | b | a | z] (cpp/kernels/qwen35_delta.cuh:77-86).
+  const std::size_t es = dtype == RAFTINFER_DTYPE_F32 ? 4 : 2;
+  const auto *base = static_cast<const unsigned char *>(input);
+  const DeltaSources src{base, c.token_stride,
+                         base + c.conv_dim * es, c.token_stride,
+                         base + (c.conv_dim + shape.value_heads) * es, c.token_stride,
+                         base + (c.conv_dim + 2 * shape.value_heads) * es, c.token_stride};
+  dispatch(src, conv_weight, recurrent_a, dt_bias, norm_w, output, conv_state, rec_state, workspace,
+           shape, c, policy, dtype, weight_dtype, stream);
+}
+
+void qwen35_gated_delta_unpacked(const void *qkv, const void *beta, const void *alpha,
+                                 const void *gate, const void *conv_weight, const void *recurrent_a,
+                                 const void *dt_bias, const void *norm_w, void *output,
+                                 float *conv_state, float *rec_state, void *workspace,
+                                 std::size_t workspace_bytes, GatedDeltaShape shape,
+                                 GatedDeltaLaunchPolicy policy, RaftInferDataType dtype,
+                                 RaftInferDataType weight_dtype, hipStream_t stream) {
+  const CheckedShape c = validate_call(
+      [&] {
+        // the pack's own pointer checks (cpp/kernels/qwen35_primitives.cu:768-800)
+        require<Err>(qkv != nullptr, "gated-delta qkv pointer is null");
+        require<Err>(beta != nullptr, "gated-delta beta pointer is null");
+        require<Err>(alpha != nullptr, "gated-delta alpha pointer is null");
+        require<Err>(gate != nullptr, "gated-delta gate pointer is null");
+      },
+      [&](std::size_t da) {
+        require_aligned(qkv, da, "gated-delta qkv is not dtype-aligned");
+        require_aligned(beta, da, "gated-delta beta is not dtype-aligned");
+        require_aligned(alpha, da, "gated-delta alpha is not dtype-aligned");
+        require_aligned(gate, da, "gated-delta gate is not dtype-aligned");
+      },
+      conv_weight, recurrent_a, dt_bias, norm_w, output, conv_state, rec_state, workspace,
+      workspace_bytes, shape, policy, dtype, weight_dtype, stream);
+  // The projection outputs, each [tokens][width]: qkv conv_dim wide, beta and
+  // alpha value_heads wide, gate hidden_size wide.
+  const DeltaSources src{qkv, c.conv_dim, beta, shape.value_heads, alpha, shape.value_heads,
+                         gate, shape.hidden_size};
+  dispatch(src, conv_weight, recurrent_a, dt_bias, norm_w, output, conv_state, rec_state, workspace,
+           shape, c, policy, dtype, weight_dtype, stream);
 }
 
 // ------------------------------------------------------- core-only entry

@@ -332,6 +332,20 @@ def qwen35_gated_delta(input, conv_weight, recurrent_a, dt_bias, output_norm_wei
             *common, policy.c(), dtype, weight_dtype, _stream(stream)))
 
 
+def qwen35_gated_delta_unpacked(qkv, beta, alpha, gate, conv_weight, recurrent_a, dt_bias,
+                                output_norm_weight, output, convolution_state, recurrent_state,
+                                workspace, shape: GatedDeltaShape, dtype: int, weight_dtype: int,
+                                policy: GatedDeltaLaunchPolicy | None = None, stream=None) -> None:
+    """qwen35_pack_linear_delta_input + qwen35_gated_delta in one call, reading the four
+    projection outputs in place (no packed copy)."""
+    policy = policy or GatedDeltaLaunchPolicy()
+    _call(Qwen35DeltaError, _lib.load().raftinfer_amd_gated_delta_unpacked(
+        _ptr(qkv), _ptr(beta), _ptr(alpha), _ptr(gate), _ptr(conv_weight), _ptr(recurrent_a),
+        _ptr(dt_bias), _ptr(output_norm_weight), _ptr(output), _fptr(convolution_state),
+        _fptr(recurrent_state), _ptr(workspace), _nbytes(workspace), shape.c(), policy.c(), dtype,
+        weight_dtype, _stream(stream)))
+
+
 def qwen35_gated_delta_core(q, k, v, beta, log_decay, q_scale, state, output, workspace=None,
                             chunked=True, stream=None) -> None:
     T, hk, dk = q.shape

@@ -229,3 +229,50 @@ def test_cfg5_full_entry_prefill_512_then_32_decode_steps(gpu):
         assert close_enough(go, wo), f"decode step {step}"
     assert rel_l2(g_rec, w_rec) < 1e-4
     assert np.array_equal(g_conv, w_conv) or rel_l2(g_conv, w_conv) < 1e-6
+
+
+@pytest.mark.parametrize("sh", [small_shape(4), model_shape(1), model_shape(3), model_shape(100),
+                                model_shape(512)], ids=["small4", "m1", "m3", "m100", "m512"])
+@pytest.mark.parametrize("dt", [1, 3])
+def test_unpacked_entry_equals_pack_then_delta(gpu, sh, dt):
+    # qwen35_gated_delta_unpacked reads the four projection outputs in place; it must give
+    # exactly what qwen35_pack_linear_delta_input + qwen35_gated_delta give
+    # (cpp/kernels/qwen35_primitives.cu:388-420, cpp/kernels/qwen35_delta.cu:811-897): the
+    # same kernels run, only the row addressing differs, so outputs and states are compared
+    # bit for bit, and the packed path against the oracle.
+    T = sh["tokens"]
+    cd = 2 * sh["hk"] * sh["dk"] + sh["hv"] * sh["dv"]
+    r = rng(T * 31 + dt)
+    qkv, beta = normal(r, T, cd), normal(r, T, sh["hv"])
+    alpha, gate = normal(r, T, sh["hv"]), normal(r, T, sh["hidden"])
+    fx = fixture_for(sh, seed=T + 11)
+    fx["inp"] = orc.pack_linear_delta_input(qkv, beta, alpha, gate).ravel()
+    conv0 = normal(r, cd * (sh["width"] - 1))
+    rec0 = normal(r, sh["hv"] * sh["dk"] * sh["dv"], scale=0.05)
+    want = run_gpu(sh, fx, dt, dt, conv0, rec0)
+    check(want, run_ref(sh, fx, dt, dt, conv0, rec0))
+    shape = ops.GatedDeltaShape(T, sh["hidden"], sh["hk"], sh["hv"], sh["dk"], sh["dv"], sh["width"],
+                                sh["eps"])
+    conv = to_dev(conv0, torch.float32)
+    rec = to_dev(rec0, torch.float32)
+    ws = torch.empty(ops.qwen35_gated_delta_workspace_bytes(shape) // 4, device="cuda")
+    out = torch.empty(T * sh["hidden"], device="cuda", dtype=TDT[dt])
+    t = lambda a: to_dev(a, TDT[dt])
+    ops.qwen35_gated_delta_unpacked(t(qkv), t(beta), t(alpha), t(gate), t(fx["cw"]), t(fx["a"]),
+                                    t(fx["dt"]), t(fx["nw"]), out, conv, rec, ws, shape, dt, dt)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_dev(out), want[0])
+    assert np.array_equal(from_dev(conv), want[1])
+    assert np.array_equal(from_dev(rec), want[2])
+
+
+def test_unpacked_entry_validation(gpu):
+    shape = ops.GatedDeltaShape(2, 4096, 16, 32, 128, 128, 4, 1e-6)
+    z = torch.zeros(2 * 12352, device="cuda", dtype=torch.bfloat16)
+    st = torch.zeros(32 * 128 * 128, device="cuda")
+    ws = torch.empty(ops.qwen35_gated_delta_workspace_bytes(shape), device="cuda", dtype=torch.uint8)
+    with pytest.raises(ops.Qwen35DeltaError, match="beta pointer is null"):
+        ops.qwen35_gated_delta_unpacked(z, None, z, z, z, z, z, z, z, st, st, ws, shape, 3, 3)
+    with pytest.raises(ops.Qwen35DeltaError, match="alpha is not dtype-aligned"):
+        # f32 activations need 4-byte alignment; one bf16 element in is 2-byte aligned
+        ops.qwen35_gated_delta_unpacked(z, z, z[1:], z, z, z, z, z, z, st, st, ws, shape, 1, 1)
