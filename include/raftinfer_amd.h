@@ -176,6 +176,23 @@ int raftinfer_amd_online_attention_decode_batched(
     void *kv_cache, size_t kv_cache_bytes, const uint32_t *context_lengths, void *workspace,
     size_t workspace_bytes, raftinfer_amd_batched_decode_shape shape, int activation_dtype,
     void *stream);
+/* Producers fused into the attention (additive; see qwen35_online_attention.hpp):
+ * q / gate split + RMSNorm + partial RoPE of q and k done inside the attention
+ * kernels, bit-identical to qwen35_split_query_gate_norm_rope /
+ * qwen35_qk_norm_rope followed by the unfused call. */
+typedef struct raftinfer_amd_fused_norm_rope {
+  const void *query_norm_weight, *key_norm_weight;
+  int weight_dtype; /* RAFTINFER_AMD_DTYPE_BF16 or _F32 */
+  size_t rotary_dim;
+  float rope_base, epsilon;
+} raftinfer_amd_fused_norm_rope;
+int raftinfer_amd_online_attention_decode_fused(
+    const void *query_gate, const void *key, const void *value, void *output, void *kv_cache,
+    size_t kv_cache_bytes, void *workspace, size_t workspace_bytes,
+    raftinfer_amd_attention_shape shape, raftinfer_amd_fused_norm_rope norm, uint8_t cache_dtype,
+    uint8_t cache_layout, raftinfer_amd_decode_plan plan, const uint32_t *device_position,
+    void *stream);
+
 /* Allocation-free decode.  No counterpart in the reference: for callers that
  * cannot allocate device memory (HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  As raftinfer_amd_online_attention_decode

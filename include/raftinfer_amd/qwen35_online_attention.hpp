@@ -95,6 +95,37 @@ void qwen35_online_attention_decode_batched(const void *query, const void *key,
                                             RaftInferDataType activation_dtype,
                                             hipStream_t stream);
 
+// ---- Additive: producers fused into the attention (no counterpart in the
+// reference). ----
+// The RMSNorm + NeoX partial RoPE of q and k (qwen35_qk_norm_rope) and the
+// q / gate split (qwen35_split_full_query_gate), which the reference runs as
+// separate kernels before the attention (cpp/execution/qwen35_executor.cu:
+// 1989-2013), done inside the attention kernels: the raw projections are read
+// once and no intermediate q / gate / k buffer exists.  Results are bit-
+// identical to the producers followed by the unfused call.  bf16 activations
+// and a bf16 KV cache, the model signature, rotary_dim a multiple of 8 (at
+// most 256); RoPE positions are past_tokens + t (decode: the device position
+// when one is given).
+struct Qwen35FusedNormRope {
+  const void *query_norm_weight; // [head_dim]
+  const void *key_norm_weight;   // [head_dim]
+  RaftInferDataType weight_dtype; // bf16 or f32
+  std::size_t rotary_dim;
+  float rope_base;
+  float epsilon;
+};
+// query_gate: [16][2][256] (query half then gate half per head, the q
+// projection's layout); key: the raw k projection [4][256]; value [4][256].
+// Otherwise as qwen35_online_attention_decode with a plan.
+void qwen35_online_attention_decode_fused(const void *query_gate, const void *key,
+                                          const void *value, void *output, void *kv_cache,
+                                          std::size_t kv_cache_bytes, void *workspace,
+                                          std::size_t workspace_bytes, Qwen35AttentionShape shape,
+                                          Qwen35FusedNormRope norm, Qwen35KvCacheDType cache_dtype,
+                                          Qwen35KvCacheLayout cache_layout,
+                                          Qwen35OnlineDecodePlan plan,
+                                          const std::uint32_t *device_position, hipStream_t stream);
+
 // Allocation-free decode (no counterpart in the reference): for callers that
 // cannot allocate device memory (code under HIP graph capture, tight serving
 // loops, harnesses that forbid hipMalloc).  Same arguments and behaviour as

@@ -68,6 +68,11 @@ class QkNormRopeShape(ctypes.Structure):
                 ("position_offset", _sz), ("rope_base", ctypes.c_float)]
 
 
+class FusedNormRope(ctypes.Structure):
+    _fields_ = [("query_norm_weight", _vp), ("key_norm_weight", _vp), ("weight_dtype", ctypes.c_int),
+                ("rotary_dim", _sz), ("rope_base", ctypes.c_float), ("epsilon", ctypes.c_float)]
+
+
 class DecodeBuffers(ctypes.Structure):
     _fields_ = [("query", _vp), ("key", _vp), ("value", _vp), ("gate", _vp), ("output", _vp),
                 ("kv_cache", _vp), ("kv_cache_bytes", _sz), ("workspace", _vp),
@@ -105,6 +110,8 @@ SIGNATURES = {
         ([_vp] * 6 + [_sz, _PU32, _vp, _sz, BatchedDecodeShape, _I, _vp], _I),
     "raftinfer_amd_online_attention_decode_partition_only":
         ([_vp] * 6 + [_sz, _vp, _sz, AttentionShape, _I, _u8, _u8, DecodePlan, _PU32, _vp], _I),
+    "raftinfer_amd_online_attention_decode_fused":
+        ([_vp] * 5 + [_sz, _vp, _sz, AttentionShape, FusedNormRope, _u8, _u8, DecodePlan, _PU32, _vp], _I),
     "raftinfer_amd_online_attention_static_workspace_bytes": ([], _sz),
     "raftinfer_amd_online_attention_decode_static_workspace":
         ([_vp] * 6 + [_sz, AttentionShape, _I, _u8, _u8, DecodePlan, _PU32, _vp], _I),

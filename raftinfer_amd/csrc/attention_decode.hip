@@ -8,9 +8,11 @@
 // query heads of the GQA group, so each K/V byte is read from HBM once.
 #include "decode_mfma.hpp"
 #include "decode_scan.hpp"
+#include "norm_rope.hpp"
 #include "raftinfer_amd/qwen35_online_attention.hpp"
 
 #include <atomic>
+#include <cmath>
 #include <mutex>
 
 namespace raftinfer::kernels {
@@ -248,7 +250,8 @@ __device__ __forceinline__ void merge_head(int d, const float *__restrict__ pmax
 
 template <typename ActT, int CH>
 __global__ __launch_bounds__(kMergeDims) void decode_merge_kernel(
-    const ActT *__restrict__ gate, ActT *__restrict__ output, const float *__restrict__ pmax,
+    const ActT *__restrict__ gate, std::size_t gate_stride, ActT *__restrict__ output,
+    const float *__restrict__ pmax,
     const float *__restrict__ psum, const float *__restrict__ pval, std::size_t max_ctx,
     std::size_t host_position, std::size_t partition_tokens, std::size_t max_partitions,
     std::size_t capacity, std::size_t threshold, const std::uint32_t *device_position) {
@@ -266,7 +269,7 @@ __global__ __launch_bounds__(kMergeDims) void decode_merge_kernel(
     Elem<ActT>::store(output, out_idx, __builtin_nanf(""));
     return;
   }
-  const float gv = Elem<ActT>::load(gate, out_idx);
+  const float gv = Elem<ActT>::load(gate, head * gate_stride + d);
   float l, a;
   merge_head<CH>(d, pmax, psum, pval, head * max_partitions, active, l, a);
   Elem<ActT>::store(output, out_idx, (a / l) * sigmoid_gate(gv));
@@ -360,7 +363,8 @@ __device__ __forceinline__ float combine_rows(const RowMergeShared<W> &sh, int d
 
 template <typename ActT, int W>
 __global__ __launch_bounds__(W * 64) void decode_merge_rows_kernel(
-    const ActT *__restrict__ gate, ActT *__restrict__ output, const float *__restrict__ pmax,
+    const ActT *__restrict__ gate, std::size_t gate_stride, ActT *__restrict__ output,
+    const float *__restrict__ pmax,
     const float *__restrict__ psum, const float *__restrict__ pval, std::size_t max_ctx,
     std::size_t host_position, std::size_t partition_tokens, std::size_t max_partitions,
     std::size_t capacity, std::size_t threshold, const std::uint32_t *device_position) {
@@ -379,7 +383,7 @@ __global__ __launch_bounds__(W * 64) void decode_merge_rows_kernel(
     if (finisher) Elem<ActT>::store(output, out_idx, __builtin_nanf(""));
     return;
   }
-  const float gv = finisher ? Elem<ActT>::load(gate, out_idx) : 0.f;
+  const float gv = finisher ? Elem<ActT>::load(gate, head * gate_stride + d) : 0.f;
   merge_rows<W>(pmax, psum, pval, head * max_partitions, active, sh);
   __syncthreads();
   if (finisher) Elem<ActT>::store(output, out_idx, combine_rows<W>(sh, d) * sigmoid_gate(gv));
@@ -404,11 +408,82 @@ __device__ __forceinline__ void append_rows(const DecodeMfmaArgs &a, std::size_t
   }
 }
 
-template <int DS, int WAVES>
+// The producers fused into a decode step (qwen35_split_query_gate_norm_rope of
+// q and qwen35_qk_norm_rope of k, cpp/kernels/qwen35_primitives.cu:158-210):
+// the raw q projection rows [16][2][256] (the query half is normalised and
+// rotated in the kernel, the gate half read by the output stage), the raw key
+// row [4][256], the norm weights and the RoPE parameters.
+struct FusedNormRope {
+  const bf16_bits *query_gate;
+  const bf16_bits *key;
+  const void *q_weight;
+  const void *k_weight;
+  bool weight_f32;
+  int pairs;    // rotary_dim / 2
+  double ratio; // rope_base^(-2 / rotary_dim)
+  float epsilon;
+};
+
+// RMSNorm + RoPE of the group's four q heads and of its key row at
+// `position`, into LDS (waves 0..3: q heads, wave 4: k; the workgroup has at
+// least 5 waves), with exactly the arithmetic of the producer kernels.
+__device__ __forceinline__ void fused_qk_prologue(const FusedNormRope &f, std::size_t kv_head,
+                                                  std::size_t position, DecodeFusedQK &fq) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  float x[4] = {0.f, 0.f, 0.f, 0.f}, w[4] = {0.f, 0.f, 0.f, 0.f};
+  if (wave <= kGroup) {
+    const bf16_bits *src = wave < kGroup ? f.query_gate + (kv_head * kGroup + wave) * 2 * kHeadDim
+                                         : f.key + kv_head * kHeadDim;
+    const u32x2 r = *reinterpret_cast<const u32x2 *>(src + 4 * lane);
+    x[0] = bf16_lo(r[0]); x[1] = bf16_hi(r[0]); x[2] = bf16_lo(r[1]); x[3] = bf16_hi(r[1]);
+    const void *wp = wave < kGroup ? f.q_weight : f.k_weight;
+    if (f.weight_f32) {
+      const float4 ww = reinterpret_cast<const float4 *>(wp)[lane];
+      w[0] = ww.x; w[1] = ww.y; w[2] = ww.z; w[3] = ww.w;
+    } else {
+      const u32x2 ww = reinterpret_cast<const u32x2 *>(wp)[lane];
+      w[0] = bf16_lo(ww[0]); w[1] = bf16_hi(ww[0]); w[2] = bf16_lo(ww[1]); w[3] = bf16_hi(ww[1]);
+    }
+  }
+  if (tid < f.pairs) {
+    float cs, sn;
+    rope_cos_sin(tid, position, f.ratio, cs, sn);
+    fq.rot[tid] = cs;
+    fq.rot[f.pairs + tid] = sn;
+  }
+  __syncthreads();
+  if (wave <= kGroup) {
+    float v[4];
+    norm_rope_256_lane(x, w, lane, f.pairs, fq.rot, f.epsilon, v);
+    bf16_bits *dst = wave < kGroup ? fq.q[wave] : fq.k;
+    *reinterpret_cast<u32x2 *>(dst + 4 * lane) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  }
+  __syncthreads();
+}
+
+// The fused form of append_rows: the key row comes from LDS (normalised and
+// rotated by fused_qk_prologue), the value row from the input.
+__device__ __forceinline__ void append_rows_fused(const DecodeMfmaArgs &a, const DecodeFusedQK &fq,
+                                                  std::size_t kv_head, std::size_t pos) {
+  const int t = threadIdx.x;
+  if (t < kHeadDim / 8) {
+    const std::size_t row = cache_row(a.head_major, pos, kv_head, a.max_ctx) + 8 * t;
+    const std::size_t plane = a.max_ctx * kKvHeads * kHeadDim;
+    *reinterpret_cast<u32x4 *>(a.cache_rw + row) = *reinterpret_cast<const u32x4 *>(&fq.k[8 * t]);
+    *reinterpret_cast<u32x4 *>(a.cache_rw + plane + row) =
+        *reinterpret_cast<const u32x4 *>(a.value_new + kv_head * kHeadDim + 8 * t);
+  }
+}
+
+// gate: element (head h, dim d) at gate[h * gate_stride + d] (gate_stride 256
+// for a split gate, 512 for the gate half of a q projection row).
+template <int DS, int WAVES, bool kFused = false>
 __global__ __launch_bounds__(WAVES * 64) void decode_single_mfma_kernel(
-    DecodeMfmaArgs a, const bf16_bits *__restrict__ gate, bf16_bits *__restrict__ output,
-    std::size_t host_position, const std::uint32_t *device_position, std::size_t threshold) {
+    DecodeMfmaArgs a, const bf16_bits *__restrict__ gate, std::size_t gate_stride,
+    bf16_bits *__restrict__ output, std::size_t host_position, const std::uint32_t *device_position,
+    std::size_t threshold, FusedNormRope f) {
   __shared__ DecodeMfmaShared<DS, WAVES> sh;
+  __shared__ DecodeFusedQK fq;
   constexpr int DIMS = kHeadDim / DS;
   const std::size_t position = read_position(device_position, host_position);
   if (position >= a.max_ctx) return;
@@ -427,13 +502,19 @@ __global__ __launch_bounds__(WAVES * 64) void decode_single_mfma_kernel(
     const int o = threadIdx.x + n * WAVES * 64;
     gv[n] = 0.f;
     if (o < kGroup * DIMS)
-      gv[n] = bf16_to_f32(gate[(kv_head * kGroup + o / DIMS) * kHeadDim + dq * DIMS + o % DIMS]);
+      gv[n] = bf16_to_f32(gate[(kv_head * kGroup + o / DIMS) * gate_stride + dq * DIMS + o % DIMS]);
   }
-  decode_mfma_scan<DS, WAVES>(a, kv_head, dq, 0, ctx, position, sh);
+  if constexpr (kFused) fused_qk_prologue(f, kv_head, position, fq);
+  decode_mfma_scan<DS, WAVES, 32, kFused>(a, kv_head, dq, 0, ctx, position, sh, &fq);
   __syncthreads();
   // The scan read the new row from key/value; the cache copy goes last so its
   // load latency is not on the critical path.
-  if (dq == 0) append_rows(a, kv_head, position);
+  if (dq == 0) {
+    if constexpr (kFused)
+      append_rows_fused(a, fq, kv_head, position);
+    else
+      append_rows(a, kv_head, position);
+  }
 #pragma unroll
   for (int n = 0; n < kOut; ++n) {
     const int o = threadIdx.x + n * WAVES * 64;
@@ -446,13 +527,14 @@ __global__ __launch_bounds__(WAVES * 64) void decode_single_mfma_kernel(
   }
 }
 
-template <int DS, int WAVES, int CT = 32>
+template <int DS, int WAVES, int CT = 32, bool kFused = false>
 __global__ __launch_bounds__(WAVES * 64) void decode_split_mfma_kernel(
     DecodeMfmaArgs a, float *__restrict__ pmax, float *__restrict__ psum,
     float *__restrict__ pval, std::size_t host_position, const std::uint32_t *device_position,
     std::size_t capacity, std::size_t max_partitions, std::size_t partition_tokens,
-    std::size_t threshold) {
+    std::size_t threshold, FusedNormRope f) {
   __shared__ DecodeMfmaShared<DS, WAVES, CT> sh;
+  __shared__ DecodeFusedQK fq;
   constexpr int DIMS = kHeadDim / DS;
   const std::size_t position = read_position(device_position, host_position);
   if (position >= a.max_ctx) return;
@@ -467,7 +549,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_mfma_kernel(
   const std::size_t begin = partition * partition_tokens;
   if (begin >= ctx) return;
   const std::size_t end = ctx < begin + partition_tokens ? ctx : begin + partition_tokens;
-  decode_mfma_scan<DS, WAVES, CT>(a, kv_head, dq, begin, end, position, sh);
+  if constexpr (kFused) fused_qk_prologue(f, kv_head, position, fq);
+  decode_mfma_scan<DS, WAVES, CT, kFused>(a, kv_head, dq, begin, end, position, sh, &fq);
   __syncthreads();
   // The workgroup whose range holds the position appends the new row.  When a
   // device position lies beyond the plan's capacity no workgroup holds it (the
@@ -476,7 +559,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_mfma_kernel(
   // kernel guarantees (cpp/kernels/qwen35_online_attention.cu:936-945).
   const bool owns_position = position >= begin && position < end;
   const bool past_capacity = partition + 1 == capacity && position >= begin + partition_tokens;
-  if (dq == 0 && (owns_position || past_capacity)) append_rows(a, kv_head, position);
+  if (dq == 0 && (owns_position || past_capacity)) {
+    if constexpr (kFused)
+      append_rows_fused(a, fq, kv_head, position);
+    else
+      append_rows(a, kv_head, position);
+  }
   for (int o = threadIdx.x; o < kGroup * DIMS; o += WAVES * 64) {
     const int h = o / DIMS, d = o % DIMS;
     float mm, l, acc;
@@ -497,18 +585,73 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_mfma_kernel(
 // 8-wave row merge, which reads whole partial rows and holds 128 partitions
 // in one round trip (ctx 16384: 20.9 -> 19.8 us per call).
 template <typename ActT>
-void launch_merge(const ActT *g, ActT *out, const float *pmax, const float *psum, const float *pval,
-                  Qwen35AttentionShape shape, Qwen35OnlineDecodePlan plan, std::size_t max_partitions,
+void launch_merge(const ActT *g, std::size_t gate_stride, ActT *out, const float *pmax,
+                  const float *psum, const float *pval, Qwen35AttentionShape shape,
+                  Qwen35OnlineDecodePlan plan, std::size_t max_partitions,
                   const std::uint32_t *device_position, hipStream_t stream) {
   constexpr unsigned grid = kQueryHeads * (kHeadDim / kMergeDims);
   if (plan.active_partition_capacity <= static_cast<std::size_t>(kMergeChunkShort))
     decode_merge_kernel<ActT, kMergeChunkShort><<<grid, kMergeDims, 0, stream>>>(
-        g, out, pmax, psum, pval, shape.max_context_tokens, shape.past_tokens, plan.partition_tokens,
+        g, gate_stride, out, pmax, psum, pval, shape.max_context_tokens, shape.past_tokens, plan.partition_tokens,
         max_partitions, plan.active_partition_capacity, plan.split_k_threshold_tokens, device_position);
   else
     decode_merge_rows_kernel<ActT, kLongMergeWaves><<<kQueryHeads, kLongMergeWaves * 64, 0, stream>>>(
-        g, out, pmax, psum, pval, shape.max_context_tokens, shape.past_tokens, plan.partition_tokens,
+        g, gate_stride, out, pmax, psum, pval, shape.max_context_tokens, shape.past_tokens, plan.partition_tokens,
         max_partitions, plan.active_partition_capacity, plan.split_k_threshold_tokens, device_position);
+}
+
+// bf16 activations and cache: single-block and / or split-K MFMA kernels of
+// the plan, then the merge.  kFused: q and k are normalised and rotated in
+// the kernels (fused producers) and the gate is the q projection's second half.
+template <bool kFused>
+void launch_decode_mfma(const DecodeMfmaArgs &args, const bf16_bits *g, std::size_t gate_stride,
+                        bf16_bits *out, void *workspace, Qwen35AttentionShape shape,
+                        Qwen35OnlineDecodePlan plan, Qwen35OnlineDecodeWorkspaceLayout ws,
+                        const std::uint32_t *device_position, hipStream_t stream,
+                        bool partition_only, FusedNormRope f) {
+  const std::size_t host_ctx = shape.past_tokens + 1;
+  const bool dynamic = device_position != nullptr;
+  const bool single = plan.resolved_mode == Qwen35DecodeAttentionMode::single_block;
+  if (partition_only) require<Err>(!single, "partition-only decode needs a split-K plan");
+  if (!partition_only && (dynamic || single || host_ctx < plan.split_k_threshold_tokens)) {
+    decode_single_mfma_kernel<kSingleDs, kSingleMfmaWaves, kFused>
+        <<<xcd_grid<kSingleDs>(kKvHeads), kSingleMfmaWaves * 64, 0, stream>>>(
+            args, g, gate_stride, out, shape.past_tokens, device_position,
+            plan.split_k_threshold_tokens, f);
+    check_launch<Err>("qwen35_online_attention_decode_gfx950_hd256");
+  }
+  if (single || (!dynamic && host_ctx < plan.split_k_threshold_tokens)) return;
+  const std::size_t max_partitions = ceil_div(shape.max_context_tokens, plan.partition_tokens,
+                                              "online decode maximum partition capacity overflow");
+  const std::size_t units = checked_mul<Err>(kKvHeads, plan.active_partition_capacity,
+                                             "online decode partition grid dimension overflow");
+  (void)grid_dim(checked_mul<Err>(units + 8, kSplitDs, "online decode partition grid dimension overflow"),
+                 "online decode partition grid dimension overflow");
+  auto *bytes = static_cast<std::byte *>(workspace);
+  auto *pmax = reinterpret_cast<float *>(bytes + ws.max_offset_bytes);
+  auto *psum = reinterpret_cast<float *>(bytes + ws.sum_offset_bytes);
+  auto *pval = reinterpret_cast<float *>(bytes + ws.value_offset_bytes);
+  // Slice the dims only while the partitions alone leave the 256 CUs idle.
+  if (units >= 192)
+    decode_split_mfma_kernel<1, kSplitWaves, 32, kFused><<<xcd_grid<1>(units), kSplitWaves * 64, 0, stream>>>(
+        args, pmax, psum, pval, shape.past_tokens, device_position, plan.active_partition_capacity,
+        max_partitions, plan.partition_tokens, plan.split_k_threshold_tokens, f);
+  else if (units >= 96)
+    decode_split_mfma_kernel<2, kSplitWaves, 32, kFused><<<xcd_grid<2>(units), kSplitWaves * 64, 0, stream>>>(
+        args, pmax, psum, pval, shape.past_tokens, device_position, plan.active_partition_capacity,
+        max_partitions, plan.partition_tokens, plan.split_k_threshold_tokens, f);
+  else
+    decode_split_mfma_kernel<kSplitDs, kSplitWaves, 32, kFused>
+        <<<xcd_grid<kSplitDs>(units), kSplitWaves * 64, 0, stream>>>(
+            args, pmax, psum, pval, shape.past_tokens, device_position, plan.active_partition_capacity,
+            max_partitions, plan.partition_tokens, plan.split_k_threshold_tokens, f);
+  check_launch<Err>(plan.partition_tokens == 256
+                        ? "qwen35_online_attention_decode_split_k_256_partition"
+                        : "qwen35_online_attention_decode_split_k_512_partition");
+  if (partition_only) return;
+  launch_merge<bf16_bits>(g, gate_stride, out, pmax, psum, pval, shape, plan, max_partitions,
+                          device_position, stream);
+  check_launch<Err>("qwen35_online_attention_decode_split_k_merge");
 }
 
 constexpr int kSingleHeads = 1, kSingleWaves = 16, kSingleUnroll = 2;
@@ -529,50 +672,8 @@ void launch_decode(const void *query, const void *key, const void *value, const 
     const DecodeMfmaArgs args{q, static_cast<const bf16_bits *>(key),
                               static_cast<const bf16_bits *>(value), cache, cache,
                               shape.max_context_tokens, head_major};
-    const std::size_t host_ctx = shape.past_tokens + 1;
-    const bool dynamic = device_position != nullptr;
-    const bool single = plan.resolved_mode == Qwen35DecodeAttentionMode::single_block;
-    if (partition_only) require<Err>(!single, "partition-only decode needs a split-K plan");
-    if (!partition_only && (dynamic || single || host_ctx < plan.split_k_threshold_tokens)) {
-      decode_single_mfma_kernel<kSingleDs, kSingleMfmaWaves>
-          <<<xcd_grid<kSingleDs>(kKvHeads), kSingleMfmaWaves * 64, 0, stream>>>(
-              args, g, out, shape.past_tokens, device_position, plan.split_k_threshold_tokens);
-      check_launch<Err>("qwen35_online_attention_decode_gfx950_hd256");
-    }
-    if (single || (!dynamic && host_ctx < plan.split_k_threshold_tokens)) return;
-    const std::size_t max_partitions = ceil_div(shape.max_context_tokens, plan.partition_tokens,
-                                                "online decode maximum partition capacity overflow");
-    const std::size_t units = checked_mul<Err>(kKvHeads, plan.active_partition_capacity,
-                                               "online decode partition grid dimension overflow");
-    (void)grid_dim(checked_mul<Err>(units + 8, kSplitDs, "online decode partition grid dimension overflow"),
-                   "online decode partition grid dimension overflow");
-    auto *bytes = static_cast<std::byte *>(workspace);
-    auto *pmax = reinterpret_cast<float *>(bytes + ws.max_offset_bytes);
-    auto *psum = reinterpret_cast<float *>(bytes + ws.sum_offset_bytes);
-    auto *pval = reinterpret_cast<float *>(bytes + ws.value_offset_bytes);
-    // Slice the dims only while the partitions alone leave the 256 CUs idle.
-    if (units >= 192)
-      decode_split_mfma_kernel<1, kSplitWaves><<<xcd_grid<1>(units), kSplitWaves * 64, 0, stream>>>(
-          args, pmax, psum, pval, shape.past_tokens, device_position,
-          plan.active_partition_capacity, max_partitions, plan.partition_tokens,
-          plan.split_k_threshold_tokens);
-    else if (units >= 96)
-      decode_split_mfma_kernel<2, kSplitWaves><<<xcd_grid<2>(units), kSplitWaves * 64, 0, stream>>>(
-          args, pmax, psum, pval, shape.past_tokens, device_position,
-          plan.active_partition_capacity, max_partitions, plan.partition_tokens,
-          plan.split_k_threshold_tokens);
-    else
-      decode_split_mfma_kernel<kSplitDs, kSplitWaves>
-          <<<xcd_grid<kSplitDs>(units), kSplitWaves * 64, 0, stream>>>(
-              args, pmax, psum, pval, shape.past_tokens, device_position,
-              plan.active_partition_capacity, max_partitions, plan.partition_tokens,
-              plan.split_k_threshold_tokens);
-    check_launch<Err>(plan.partition_tokens == 256
-                          ? "qwen35_online_attention_decode_split_k_256_partition"
-                          : "qwen35_online_attention_decode_split_k_512_partition");
-    if (partition_only) return;
-    launch_merge<ActT>(g, out, pmax, psum, pval, shape, plan, max_partitions, device_position, stream);
-    check_launch<Err>("qwen35_online_attention_decode_split_k_merge");
+    launch_decode_mfma<false>(args, g, kHeadDim, out, workspace, shape, plan, ws, device_position,
+                              stream, partition_only, FusedNormRope{});
     return;
   }
   if (partition_only) {
@@ -618,7 +719,8 @@ void launch_decode(const void *query, const void *key, const void *value, const 
   check_launch<Err>(plan.partition_tokens == 256
                         ? "qwen35_online_attention_decode_split_k_256_partition"
                         : "qwen35_online_attention_decode_split_k_512_partition");
-  launch_merge<ActT>(g, out, pmax, psum, pval, shape, plan, max_partitions, device_position, stream);
+  launch_merge<ActT>(g, kHeadDim, out, pmax, psum, pval, shape, plan, max_partitions, device_position,
+                     stream);
   check_launch<Err>("qwen35_online_attention_decode_split_k_merge");
 }
 
@@ -681,7 +783,7 @@ void decode_impl(const void *query, const void *key, const void *value, const vo
                  std::size_t workspace_bytes, Qwen35AttentionShape shape, RaftInferDataType act,
                  Qwen35KvCacheDType cache_dtype, Qwen35KvCacheLayout layout,
                  Qwen35OnlineDecodePlan plan, const std::uint32_t *device_position,
-                 hipStream_t stream, bool partition_only) {
+                 hipStream_t stream, bool partition_only, const FusedNormRope *fused = nullptr) {
   require<Err>(query != nullptr, "online decode query pointer is null");
   require<Err>(key != nullptr, "online decode key pointer is null");
   require<Err>(value != nullptr, "online decode value pointer is null");
@@ -737,6 +839,18 @@ void decode_impl(const void *query, const void *key, const void *value, const vo
   require_aligned16(query, "online decode query must be 16-byte aligned");
   require_aligned16(kv_cache, "online decode KV cache must be 16-byte aligned");
 
+  if (fused != nullptr) {
+    // query = the q projection rows [16][2][256]; the gate is their second half
+    require<Err>(act == RAFTINFER_DTYPE_BF16 && cache_dtype == Qwen35KvCacheDType::bf16,
+                 "fused decode requires bf16 activations and a bf16 KV cache");
+    const DecodeMfmaArgs args{nullptr, nullptr, static_cast<const bf16_bits *>(value),
+                              static_cast<bf16_bits *>(kv_cache), static_cast<bf16_bits *>(kv_cache),
+                              shape.max_context_tokens, layout == Qwen35KvCacheLayout::head_major};
+    launch_decode_mfma<true>(args, static_cast<const bf16_bits *>(query) + kHeadDim, 2 * kHeadDim,
+                             static_cast<bf16_bits *>(output), workspace, shape, plan, ws,
+                             device_position, stream, false, *fused);
+    return;
+  }
   const bool f32_act = act == RAFTINFER_DTYPE_F32;
   const bool f32_cache = cache_dtype == Qwen35KvCacheDType::f32;
   if (f32_act && f32_cache)
@@ -850,6 +964,42 @@ void qwen35_online_attention_decode_static_workspace(
   void *workspace = bytes != 0 ? scratch_for_current_device() : nullptr;
   decode_impl(query, key, value, gate, output, kv_cache, kv_cache_bytes, workspace, bytes, shape,
               activation_dtype, cache_dtype, cache_layout, plan, device_position, stream, false);
+}
+
+void qwen35_online_attention_decode_fused(const void *query_gate, const void *key,
+                                          const void *value, void *output, void *kv_cache,
+                                          std::size_t kv_cache_bytes, void *workspace,
+                                          std::size_t workspace_bytes, Qwen35AttentionShape shape,
+                                          Qwen35FusedNormRope norm, Qwen35KvCacheDType cache_dtype,
+                                          Qwen35KvCacheLayout layout, Qwen35OnlineDecodePlan plan,
+                                          const std::uint32_t *device_position, hipStream_t stream) {
+  // The producer's checks (cpp/kernels/qwen35_primitives.cu:580-601) for the
+  // parameters it adds, then the decode's own validation.
+  require<Err>(norm.query_norm_weight != nullptr && norm.key_norm_weight != nullptr,
+               "fused decode norm weight pointer is null");
+  require<Err>(norm.weight_dtype == RAFTINFER_DTYPE_BF16 || norm.weight_dtype == RAFTINFER_DTYPE_F32,
+               "fused decode norm weights must be bf16 or f32");
+  require<Err>(norm.rotary_dim > 0 && norm.rotary_dim <= kHeadDim && norm.rotary_dim % 8 == 0,
+               "fused decode rotary_dim must be a positive multiple of 8 up to 256");
+  require<Err>(std::isfinite(norm.rope_base) && norm.rope_base > 0.0f,
+               "qk_norm_rope rope_base must be finite and positive");
+  require<Err>(std::isfinite(norm.epsilon) && norm.epsilon >= 0.0f,
+               "qk_norm_rope epsilon must be finite and non-negative");
+  const std::size_t wa = norm.weight_dtype == RAFTINFER_DTYPE_F32 ? 16 : 8;
+  require<Err>(((reinterpret_cast<std::uintptr_t>(norm.query_norm_weight) |
+                 reinterpret_cast<std::uintptr_t>(norm.key_norm_weight)) & (wa - 1)) == 0,
+               "fused decode norm weights are not vector-aligned");
+  require<Err>(((reinterpret_cast<std::uintptr_t>(key) | reinterpret_cast<std::uintptr_t>(value)) & 15u) == 0,
+               "fused decode key and value must be 16-byte aligned");
+  const FusedNormRope f{static_cast<const bf16_bits *>(query_gate), static_cast<const bf16_bits *>(key),
+                        norm.query_norm_weight, norm.key_norm_weight,
+                        norm.weight_dtype == RAFTINFER_DTYPE_F32, static_cast<int>(norm.rotary_dim / 2),
+                        std::pow(static_cast<double>(norm.rope_base), -2.0 / static_cast<double>(norm.rotary_dim)),
+                        norm.epsilon};
+  const void *gate = query_gate == nullptr ? nullptr : static_cast<const bf16_bits *>(query_gate) + kHeadDim;
+  decode_impl(query_gate, key, value, gate, output, kv_cache, kv_cache_bytes, workspace,
+              workspace_bytes, shape, RAFTINFER_DTYPE_BF16, cache_dtype, layout, plan, device_position,
+              stream, false, &f);
 }
 
 std::uint32_t qwen35_online_attention_consume_capacity_errors() {

@@ -31,6 +31,15 @@ struct DecodeMfmaArgs {
   bool head_major;
 };
 
+// q of one GQA group and the new token's k after RMSNorm + RoPE, computed by
+// the decode kernel itself when the producers are fused into it; rot holds the
+// rotation table (cos then sin) of the decode position.
+struct DecodeFusedQK {
+  bf16_bits q[kGroup][kHeadDim];
+  bf16_bits k[kHeadDim];
+  float rot[kHeadDim];
+};
+
 template <int DS, int WAVES, int CT = 32> struct DecodeMfmaShared {
   static constexpr int DIMS = kHeadDim / DS;
   float p[WAVES][CT][4];
@@ -89,10 +98,14 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // over half of the line and the score is C[2t][h] + C[2t+1][4+h], two values
 // 4 lanes apart in a row (one DPP add).  After it, lane l with l%16 < 4 holds
 // head l%16's scores of tokens 2*(l/16) and 2*(l/16)+1 of the group.
-template <int DS, int WAVES, int CT = 32>
+//
+// kFused: q comes from fq->q and the new token's key row from fq->k (both in
+// LDS) instead of a.query and a.key_new.
+template <int DS, int WAVES, int CT = 32, bool kFused = false>
 __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::size_t kv_head,
                                                  int dq, std::size_t begin, std::size_t end,
-                                                 std::size_t pos, DecodeMfmaShared<DS, WAVES, CT> &sh) {
+                                                 std::size_t pos, DecodeMfmaShared<DS, WAVES, CT> &sh,
+                                                 const DecodeFusedQK *fq = nullptr) {
   constexpr int DIMS = kHeadDim / DS;
   constexpr int G = CT / 8; // 8-token groups per chunk
   // K is read non-temporally when at most 4 sibling workgroups share it
@@ -120,9 +133,13 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
 #pragma unroll
   for (int line = 0; line < 4; ++line) {
     u32x4 w = u32x4{0u, 0u, 0u, 0u};
-    if (n < 8)
-      w = *reinterpret_cast<const u32x4 *>(a.query + (kv_head * kGroup + (n & 3)) * kHeadDim + line * 64 +
-                                           (2 * kq + (n >> 2)) * 8);
+    if (n < 8) {
+      if constexpr (kFused)
+        w = *reinterpret_cast<const u32x4 *>(&fq->q[n & 3][line * 64 + (2 * kq + (n >> 2)) * 8]);
+      else
+        w = *reinterpret_cast<const u32x4 *>(a.query + (kv_head * kGroup + (n & 3)) * kHeadDim + line * 64 +
+                                             (2 * kq + (n >> 2)) * 8);
+    }
     qb[line] = __builtin_bit_cast(bf16x8, w);
   }
 
@@ -143,12 +160,25 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
     for (int g = 0; g < G; ++g) {
       std::size_t tok = c0 + 8 * g + rt;
       tok = tok < end ? tok : end - 1;
-      const bf16_bits *row = tok == pos ? a.key_new + kv_head * kHeadDim
-                                        : kplane + cache_row(a.head_major, tok, kv_head, a.max_ctx);
+      // (fused: the cache row of the new token is read too, and replaced below)
+      const bf16_bits *row = !kFused && tok == pos ? a.key_new + kv_head * kHeadDim
+                                                   : kplane + cache_row(a.head_major, tok, kv_head, a.max_ctx);
 #pragma unroll
       for (int line = 0; line < 4; ++line)
         kr[g][line] = kNtKeys ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(row + line * 64 + seg * 8))
                               : *reinterpret_cast<const u32x4 *>(row + line * 64 + seg * 8);
+    }
+    if constexpr (kFused) {
+      if (pos >= c0 && pos < c0 + CT) { // this chunk holds the new token (wave-uniform)
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          if (c0 + 8 * g + rt == pos) {
+#pragma unroll
+            for (int line = 0; line < 4; ++line)
+              kr[g][line] = *reinterpret_cast<const u32x4 *>(&fq->k[line * 64 + seg * 8]);
+          }
+        }
+      }
     }
     VRow<VEC> vv[TPL];
 #pragma unroll

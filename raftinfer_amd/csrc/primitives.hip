@@ -13,6 +13,7 @@
 // query half of a [heads][2][head_dim] q projection and copies the gate half
 // for the fused split.
 #include "common.hpp"
+#include "norm_rope.hpp"
 #include "raftinfer_amd/qwen35_primitives.hpp"
 
 #include <cmath>
@@ -142,48 +143,22 @@ __global__ __launch_bounds__(kNormThreads) void norm_rope_256_kernel(
   Vec4<Wt>::load(weight + d0, w);
   if (static_cast<int>(threadIdx.x) < pairs) {
     const int p = threadIdx.x;
-    double inv = 1.0, bsq = ratio;
-    for (int e = p; e != 0; e >>= 1, bsq *= bsq)
-      if (e & 1) inv *= bsq;
     const std::size_t position =
         (device_position != nullptr ? static_cast<std::size_t>(*device_position) : position_offset) + token;
-    const double theta = static_cast<double>(position) * inv;
-    constexpr double kTwoPi = 6.283185307179586476925286766559;
-    const double t = theta - kTwoPi * rint(theta / kTwoPi);
-    float sn, cs;
-    sincosf(static_cast<float>(t), &sn, &cs);
+    float cs, sn;
+    rope_cos_sin(p, position, ratio, cs, sn);
     rot[p] = cs;
     rot[pairs + p] = sn;
   }
   __syncthreads();
-  const int shift = pairs / 4; // lanes between a dim and its partner
-  const bool rotated = d0 < 2 * pairs, first = d0 < pairs;
-  const int src_lane = first ? lane + shift : lane - shift;
   for (std::size_t h0 = wave; h0 < heads; h0 += kWaves * kBatch) {
     if (h0 != static_cast<std::size_t>(wave)) load_batch(h0);
 #pragma unroll
     for (int b = 0; b < kBatch; ++b) {
       const std::size_t h = h0 + kWaves * b;
       if (h >= heads) break; // uniform across the wave
-      float ss = 0.f;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ss = fmaf(x[b][e], x[b][e], ss);
-      ss = wave_sum(ss);
-      const float scale = 1.0f / sqrtf(ss * (1.0f / 256.0f) + epsilon);
       float v[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = x[b][e] * scale * w[e];
-      float pv[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) pv[e] = __shfl(v[e], src_lane);
-      if (rotated) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int p = first ? d0 + e : d0 + e - pairs;
-          const float c = rot[p], sn = rot[pairs + p];
-          v[e] = first ? v[e] * c - pv[e] * sn : pv[e] * sn + v[e] * c;
-        }
-      }
+      norm_rope_256_lane(x[b], w, lane, pairs, rot, epsilon, v);
       Vec4<T>::store(output + (token * heads + h) * 256 + d0, v);
       if (gate != nullptr) Vec4<T>::store(gate + (token * heads + h) * 256 + d0, g[b]);
     }

@@ -233,6 +233,33 @@ def qwen35_online_attention_decode(query, key, value, gate, output, kv_cache, wo
         _stream(stream)))
 
 
+@dataclass
+class Qwen35FusedNormRope:
+    """The producer parameters of the fused attention entry points."""
+    query_norm_weight: object  # device tensor [head_dim]
+    key_norm_weight: object
+    rotary_dim: int
+    rope_base: float
+    epsilon: float
+
+    def c(self):
+        wd = _dtype_code(self.query_norm_weight)
+        return _lib.FusedNormRope(_ptr(self.query_norm_weight), _ptr(self.key_norm_weight), wd,
+                                  self.rotary_dim, self.rope_base, self.epsilon)
+
+
+def qwen35_online_attention_decode_fused(query_gate, key, value, output, kv_cache, workspace, shape,
+                                         norm: Qwen35FusedNormRope, cache_dtype, cache_layout, plan,
+                                         device_position=None, stream=None) -> None:
+    """The q split + RMSNorm + RoPE of q and k fused into the decode attention."""
+    pos = None if device_position is None else ctypes.cast(device_position.data_ptr(),
+                                                           ctypes.POINTER(ctypes.c_uint32))
+    _call(Qwen35PrimitiveError, _lib.load().raftinfer_amd_online_attention_decode_fused(
+        _ptr(query_gate), _ptr(key), _ptr(value), _ptr(output), _ptr(kv_cache), _nbytes(kv_cache),
+        _ptr(workspace), _nbytes(workspace), shape.c(), norm.c(), cache_dtype, cache_layout,
+        DecodePlan(*plan), pos, _stream(stream)))
+
+
 def qwen35_online_attention_static_workspace_bytes() -> int:
     return int(_lib.load().raftinfer_amd_online_attention_static_workspace_bytes())
 
