@@ -193,6 +193,11 @@ int raftinfer_amd_online_attention_decode_fused(
     uint8_t cache_layout, raftinfer_amd_decode_plan plan, const uint32_t *device_position,
     void *stream);
 
+int raftinfer_amd_online_attention_prefill_fused(
+    const void *query_gate, const void *key, const void *value, void *output, void *kv_cache,
+    size_t kv_cache_bytes, raftinfer_amd_attention_shape shape, raftinfer_amd_fused_norm_rope norm,
+    uint8_t cache_dtype, uint8_t cache_layout, void *stream);
+
 /* Allocation-free decode.  No counterpart in the reference: for callers that
  * cannot allocate device memory (HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  As raftinfer_amd_online_attention_decode

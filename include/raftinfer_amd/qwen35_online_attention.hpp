@@ -126,6 +126,16 @@ void qwen35_online_attention_decode_fused(const void *query_gate, const void *ke
                                           Qwen35OnlineDecodePlan plan,
                                           const std::uint32_t *device_position, hipStream_t stream);
 
+// query_gate: [tokens][16][2][256]; key: the raw k projection [tokens][4][256];
+// value [tokens][4][256].  The keys are normalised, rotated and appended with
+// the values at past_tokens .. past_tokens + tokens - 1, then the causal gated
+// attention runs as qwen35_online_attention_prefill.  A bf16 KV cache.
+void qwen35_online_attention_prefill_fused(const void *query_gate, const void *key,
+                                           const void *value, void *output, void *kv_cache,
+                                           std::size_t kv_cache_bytes, Qwen35AttentionShape shape,
+                                           Qwen35FusedNormRope norm, Qwen35KvCacheDType cache_dtype,
+                                           Qwen35KvCacheLayout cache_layout, hipStream_t stream);
+
 // Allocation-free decode (no counterpart in the reference): for callers that
 // cannot allocate device memory (code under HIP graph capture, tight serving
 // loops, harnesses that forbid hipMalloc).  Same arguments and behaviour as

@@ -112,6 +112,8 @@ SIGNATURES = {
         ([_vp] * 6 + [_sz, _vp, _sz, AttentionShape, _I, _u8, _u8, DecodePlan, _PU32, _vp], _I),
     "raftinfer_amd_online_attention_decode_fused":
         ([_vp] * 5 + [_sz, _vp, _sz, AttentionShape, FusedNormRope, _u8, _u8, DecodePlan, _PU32, _vp], _I),
+    "raftinfer_amd_online_attention_prefill_fused":
+        ([_vp] * 5 + [_sz, AttentionShape, FusedNormRope, _u8, _u8, _vp], _I),
     "raftinfer_amd_online_attention_static_workspace_bytes": ([], _sz),
     "raftinfer_amd_online_attention_decode_static_workspace":
         ([_vp] * 6 + [_sz, AttentionShape, _I, _u8, _u8, DecodePlan, _PU32, _vp], _I),

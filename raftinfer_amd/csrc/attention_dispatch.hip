@@ -6,6 +6,7 @@
 // prefill runs the bf16 MFMA kernel (attention_prefill_mfma.hip) for the
 // Qwen3.5 signature with bf16 activations and cache, and a generic fp32
 // wave-per-row kernel for every other supported shape / dtype / layout.
+#include <cmath>
 #include "decode_scan.hpp"
 #include "prefill_mfma.hpp"
 #include "raftinfer_amd/qwen35_online_attention.hpp"
@@ -488,6 +489,58 @@ void qwen35_online_attention_prefill_kernel_only(
     Qwen35KvCacheDType cache_dtype, Qwen35KvCacheLayout layout, hipStream_t stream) {
   prefill_impl(query, key, value, gate, output, kv_cache, kv_cache_bytes, shape, act, cache_dtype,
                layout, stream, true);
+}
+
+void qwen35_online_attention_prefill_fused(const void *query_gate, const void *key,
+                                           const void *value, void *output, void *kv_cache,
+                                           std::size_t kv_cache_bytes, Qwen35AttentionShape shape,
+                                           Qwen35FusedNormRope norm, Qwen35KvCacheDType cache_dtype,
+                                           Qwen35KvCacheLayout layout, hipStream_t stream) {
+  require<Err>(query_gate != nullptr, "online attention query pointer is null");
+  require<Err>(key != nullptr, "online attention key pointer is null");
+  require<Err>(value != nullptr, "online attention value pointer is null");
+  require<Err>(output != nullptr, "online attention output pointer is null");
+  require<Err>(kv_cache != nullptr, "online attention KV cache pointer is null");
+  require<Err>(stream != nullptr, "online attention HIP stream is null");
+  require<Err>(online_prefill_signature_supported(shape, RAFTINFER_DTYPE_BF16, cache_dtype, layout),
+               "unsupported online attention prefill signature; select the "
+               "materialized implementation before allocation");
+  require<Err>(cache_dtype == Qwen35KvCacheDType::bf16 && shape.query_heads == kQueryHeads &&
+                   shape.kv_heads == kKvHeads && shape.head_dim == kHeadDim,
+               "fused prefill requires the model signature with a bf16 KV cache");
+  const std::size_t required = checked_mul<Err>(
+      checked_mul<Err>(2, checked_mul<Err>(shape.max_context_tokens, kKvHeads * kHeadDim,
+                                           "online attention cache shape overflow"),
+                       "online attention cache shape overflow"),
+      2, "online attention cache byte size overflow");
+  require<Err>(kv_cache_bytes >= required, "online attention KV cache is too small");
+  require<Err>(norm.query_norm_weight != nullptr && norm.key_norm_weight != nullptr,
+               "fused prefill norm weight pointer is null");
+  require<Err>(norm.weight_dtype == RAFTINFER_DTYPE_BF16 || norm.weight_dtype == RAFTINFER_DTYPE_F32,
+               "fused prefill norm weights must be bf16 or f32");
+  require<Err>(norm.rotary_dim > 0 && norm.rotary_dim <= kHeadDim && norm.rotary_dim % 8 == 0,
+               "fused prefill rotary_dim must be a positive multiple of 8 up to 256");
+  require<Err>(std::isfinite(norm.rope_base) && norm.rope_base > 0.0f,
+               "qk_norm_rope rope_base must be finite and positive");
+  require<Err>(std::isfinite(norm.epsilon) && norm.epsilon >= 0.0f,
+               "qk_norm_rope epsilon must be finite and non-negative");
+  const auto bits = [](const void *p) { return reinterpret_cast<std::uintptr_t>(p); };
+  const std::size_t wa = norm.weight_dtype == RAFTINFER_DTYPE_F32 ? 16 : 8;
+  require<Err>(((bits(norm.query_norm_weight) | bits(norm.key_norm_weight)) & (wa - 1)) == 0,
+               "fused prefill norm weights are not vector-aligned");
+  require<Err>(((bits(query_gate) | bits(kv_cache)) & 15u) == 0 &&
+                   ((bits(key) | bits(value) | bits(output)) & 7u) == 0,
+               "fused prefill needs 16-byte aligned q projection and cache, 8-byte aligned key, "
+               "value and output");
+  amd::launch_prefill_mfma_fused(
+      static_cast<const bf16_bits *>(query_gate), static_cast<const bf16_bits *>(key),
+      static_cast<const bf16_bits *>(value), static_cast<bf16_bits *>(output),
+      static_cast<bf16_bits *>(kv_cache), shape.tokens, shape.max_context_tokens, shape.past_tokens,
+      layout == Qwen35KvCacheLayout::head_major, norm.query_norm_weight, norm.key_norm_weight,
+      norm.weight_dtype == RAFTINFER_DTYPE_F32, static_cast<int>(norm.rotary_dim / 2),
+      std::pow(static_cast<double>(norm.rope_base), -2.0 / static_cast<double>(norm.rotary_dim)),
+      norm.epsilon, stream);
+  check_launch<Err>("qwen35_online_attention_prefill_fused");
 }
 
 // --------------------------------------------------------- dispatcher

@@ -36,6 +36,7 @@
 // the loop.  With past == 0 the keys come from the key/value
 // inputs and each workgroup also writes its 8 tokens' cache rows (the append).
 #include "decode_scan.hpp"
+#include "norm_rope.hpp"
 #include "prefill_mfma.hpp"
 
 namespace raftinfer::amd {
@@ -65,6 +66,19 @@ struct PrefillShared {
   bf16_bits q[32 * kHeadDim]; // Q^T operand rows (one per column), swizzled like K
   float m[kWaves][kWave];
   float l[kWaves][kWave];
+};
+
+// The q producer fused into the prefill kernel (NormQ).
+struct PrefillNormRope {
+  const void *weight; // q norm weight [256], bf16 or f32
+  bool weight_f32;
+  int pairs;    // rotary_dim / 2 (rotary_dim a multiple of 8)
+  double ratio; // rope_base^(-2 / rotary_dim)
+  float epsilon;
+};
+struct NormQShared {
+  float weight[kHeadDim];        // the staged norm weight (bf16 uses the first half)
+  float rot[kQTok][kHeadDim];    // per token slot: cos[pairs] then sin[pairs]
 };
 
 // Physical 16-byte chunk of logical chunk c in tile row r: c ^ (r & 7).  An
@@ -125,13 +139,18 @@ __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(
 // compiler may sink them past the asm loads (it knows the asm cannot reach
 // restrict-only memory), and the waits would then release K/V tiles that have
 // not landed.
-template <bool HeadMajor, bool FromInput>
+//
+// NormQ: `query` is the raw q projection [tokens][16][2][256]; its query half
+// is staged like Q and normalised + rotated in LDS (the producer
+// qwen35_split_query_gate_norm_rope fused in), and the gate is its second half.
+template <bool HeadMajor, bool FromInput, bool NormQ = false>
 __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
     const bf16_bits *__restrict__ query, const bf16_bits *key_in,
     const bf16_bits *value_in, const bf16_bits *gate,
     bf16_bits *__restrict__ output, bf16_bits *__restrict__ cache, std::size_t tokens,
-    std::size_t max_ctx, std::size_t past) {
+    std::size_t max_ctx, std::size_t past, PrefillNormRope nq) {
   constexpr bool head_major = HeadMajor;
+  static_assert(!(NormQ && FromInput), "the fused producer path reads K/V from the cache");
   __shared__ PrefillShared sh;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -164,6 +183,11 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
     const std::size_t tt = static_cast<std::size_t>(c & 7) < q_rows ? static_cast<std::size_t>(c & 7) : q_rows - 1;
     return ((t0 + tt) * kQueryHeads + kv_head * kGroup + (c >> 3)) * kHeadDim;
   };
+  // Row of column c's gate: the gate input, or the second half of its q
+  // projection row.
+  const bf16_bits *gate_src = NormQ ? query + kHeadDim : gate;
+  auto gate_row = [&](int c) { return NormQ ? 2 * io_row(c) : io_row(c); };
+  constexpr std::size_t q_row_elems = NormQ ? 2 * kHeadDim : kHeadDim; // elements between Q rows
   WaveTile &tile = sh.tile[wave_u];
   constexpr int kLateLoads = 4 + (FromInput ? 2 : 0); // gate (+ append) loads per thread
 
@@ -229,9 +253,22 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
       const int r = 2 * i + half; // column of this lane's row
       const int rt = r & (kQTok - 1);
       const std::size_t rrow = static_cast<std::size_t>(rt) < q_rows ? rt : q_rows - 1;
-      const std::uint32_t voff = static_cast<std::uint32_t>(rrow * kQueryHeads + (r >> 3)) * (kHeadDim * 2) +
+      const std::uint32_t voff = static_cast<std::uint32_t>(rrow * kQueryHeads + (r >> 3)) * (q_row_elems * 2) +
                                  16u * (col ^ swz(r));
-      load_lds_b128(query + (t0 * kQueryHeads + kv_head * kGroup) * kHeadDim, voff, lq + 1024u * i);
+      load_lds_b128(query + (t0 * kQueryHeads + kv_head * kGroup) * q_row_elems, voff, lq + 1024u * i);
+    }
+  }
+  [[maybe_unused]] NormQShared *nqs = nullptr;
+  if constexpr (NormQ) {
+    // The q norm weight (512 B bf16 or 1 KiB f32) into LDS by wave 0, issued
+    // before K/V so the Q wait below covers it; lanes past the weight re-read
+    // its last piece.
+    __shared__ NormQShared nq_sh;
+    nqs = &nq_sh;
+    if (wave_u == 0) {
+      const std::uint32_t bytes = nq.weight_f32 ? 1024u : 512u;
+      const std::uint32_t off = 16u * lane < bytes ? 16u * lane : bytes - 16u;
+      load_lds_b128(nq.weight, off, lds_address(nq_sh.weight));
     }
   }
   std::size_t t = wave_u;
@@ -266,11 +303,45 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
 #pragma unroll
   for (int n = 0; n < 4; ++n) {
     const int c = 8 * n + (lane >> 3), k = lane & 7;
-    gc[n] = *reinterpret_cast<const u32x4 *>(gate + io_row(c) + 64 * wave_u + 8 * k);
+    gc[n] = *reinterpret_cast<const u32x4 *>(gate_src + gate_row(c) + 64 * wave_u + 8 * k);
   }
 
+  if constexpr (NormQ) {
+    // Rotation tables of the tile's (up to 8) positions, while Q is in flight.
+    for (int i = tid; i < kQTok * nq.pairs; i += kThreads) {
+      const int slot = i / nq.pairs, pp = i - slot * nq.pairs;
+      const std::size_t tt = static_cast<std::size_t>(slot) < q_rows ? slot : q_rows - 1;
+      float cs, sn;
+      rope_cos_sin(pp, past + t0 + tt, nq.ratio, cs, sn);
+      nqs->rot[slot][pp] = cs;
+      nqs->rot[slot][nq.pairs + pp] = sn;
+    }
+  }
   if (t < n_tiles) wait_vm<32 + kLateLoads>(); else wait_vm<0>(); // this wave's Q rows have landed
   __syncthreads(); // ... and every other wave's
+  if constexpr (NormQ) {
+    // RMSNorm + RoPE of rows 8w .. 8w+7 in place: lane l owns dims 4l .. 4l+3
+    // (8 bytes of logical chunk l / 2); bf16 results as the producer stores them.
+    float w[4];
+    if (nq.weight_f32) {
+      const float4 x = reinterpret_cast<const float4 *>(nqs->weight)[lane];
+      w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
+    } else {
+      const u32x2 x = reinterpret_cast<const u32x2 *>(nqs->weight)[lane];
+      w[0] = bf16_lo(x[0]); w[1] = bf16_hi(x[0]); w[2] = bf16_lo(x[1]); w[3] = bf16_hi(x[1]);
+    }
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) {
+      const int r = 8 * wave_u + rr;
+      u32x2 *slot = reinterpret_cast<u32x2 *>(sh.q + chunk_offset(r, lane >> 1) + 4 * (lane & 1));
+      const u32x2 raw = *slot;
+      const float x[4] = {bf16_lo(raw[0]), bf16_hi(raw[0]), bf16_lo(raw[1]), bf16_hi(raw[1])};
+      float v[4];
+      norm_rope_256_lane(x, w, lane, nq.pairs, nqs->rot[r & (kQTok - 1)], nq.epsilon, v);
+      *slot = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    }
+    __syncthreads(); // every row is normalised
+  }
   for (; t < n_tiles; t += kWaves) {
     const std::size_t k0 = t * kKTile;
     const bool more = t + kWaves < n_tiles;
@@ -517,20 +588,78 @@ void launch_prefill_mfma(const bf16_bits *q, const bf16_bits *key, const bf16_bi
                          bool head_major, bool fused_append, hipStream_t stream) {
   // 8 workgroups (one per XCD) per pair of query tiles.
   const unsigned grid = static_cast<unsigned>(8 * ceil_div_unchecked(ceil_div_unchecked(tokens, kQTok), 2));
+  const PrefillNormRope none{};
   if (fused_append) {
     if (head_major)
       prefill_mfma_kernel<true, true><<<grid, kThreads, 0, stream>>>(q, key, value, gate, out, cache,
-                                                                     tokens, max_ctx, past);
+                                                                     tokens, max_ctx, past, none);
     else
       prefill_mfma_kernel<false, true><<<grid, kThreads, 0, stream>>>(q, key, value, gate, out, cache,
-                                                                      tokens, max_ctx, past);
+                                                                      tokens, max_ctx, past, none);
   } else if (head_major) {
     prefill_mfma_kernel<true, false><<<grid, kThreads, 0, stream>>>(q, key, value, gate, out, cache,
-                                                                    tokens, max_ctx, past);
+                                                                    tokens, max_ctx, past, none);
   } else {
     prefill_mfma_kernel<false, false><<<grid, kThreads, 0, stream>>>(q, key, value, gate, out, cache,
-                                                                     tokens, max_ctx, past);
+                                                                     tokens, max_ctx, past, none);
   }
+}
+
+namespace {
+// The k producer fused with the cache append: block = token, wave h = KV
+// head h.  RMSNorm + RoPE of the raw key row (the arithmetic of
+// qwen35_qk_norm_rope) stored at position past + t of the K plane, and the
+// value row copied to the V plane.
+__global__ __launch_bounds__(256) void key_norm_rope_append_kernel(
+    const bf16_bits *__restrict__ key, const bf16_bits *__restrict__ value, const void *weight,
+    bool weight_f32, int pairs, double ratio, float epsilon, bf16_bits *__restrict__ cache,
+    std::size_t max_ctx, std::size_t past, bool head_major) {
+  __shared__ float rot[kHeadDim];
+  const std::size_t t = blockIdx.x;
+  const int lane = threadIdx.x & 63, h = threadIdx.x >> 6;
+  const std::size_t src = (t * kKvHeads + h) * kHeadDim + 4 * lane;
+  const u32x2 raw = *reinterpret_cast<const u32x2 *>(key + src);
+  const u32x2 vv = *reinterpret_cast<const u32x2 *>(value + src);
+  float w[4];
+  if (weight_f32) {
+    const float4 x = reinterpret_cast<const float4 *>(weight)[lane];
+    w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
+  } else {
+    const u32x2 x = reinterpret_cast<const u32x2 *>(weight)[lane];
+    w[0] = bf16_lo(x[0]); w[1] = bf16_hi(x[0]); w[2] = bf16_lo(x[1]); w[3] = bf16_hi(x[1]);
+  }
+  if (static_cast<int>(threadIdx.x) < pairs) {
+    float cs, sn;
+    rope_cos_sin(threadIdx.x, past + t, ratio, cs, sn);
+    rot[threadIdx.x] = cs;
+    rot[pairs + threadIdx.x] = sn;
+  }
+  __syncthreads();
+  const float x[4] = {bf16_lo(raw[0]), bf16_hi(raw[0]), bf16_lo(raw[1]), bf16_hi(raw[1])};
+  float v[4];
+  norm_rope_256_lane(x, w, lane, pairs, rot, epsilon, v);
+  const std::size_t row = cache_row(head_major, past + t, h, max_ctx) + 4 * lane;
+  *reinterpret_cast<u32x2 *>(cache + row) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  *reinterpret_cast<u32x2 *>(cache + max_ctx * kKvHeads * kHeadDim + row) = vv;
+}
+} // namespace
+
+void launch_prefill_mfma_fused(const bf16_bits *query_gate, const bf16_bits *key,
+                               const bf16_bits *value, bf16_bits *out, bf16_bits *cache,
+                               std::size_t tokens, std::size_t max_ctx, std::size_t past,
+                               bool head_major, const void *q_weight, const void *k_weight,
+                               bool weight_f32, int pairs, double ratio, float epsilon,
+                               hipStream_t stream) {
+  key_norm_rope_append_kernel<<<static_cast<unsigned>(tokens), 256, 0, stream>>>(
+      key, value, k_weight, weight_f32, pairs, ratio, epsilon, cache, max_ctx, past, head_major);
+  const unsigned grid = static_cast<unsigned>(8 * ceil_div_unchecked(ceil_div_unchecked(tokens, kQTok), 2));
+  const PrefillNormRope nq{q_weight, weight_f32, pairs, ratio, epsilon};
+  if (head_major)
+    prefill_mfma_kernel<true, false, true><<<grid, kThreads, 0, stream>>>(
+        query_gate, key, value, nullptr, out, cache, tokens, max_ctx, past, nq);
+  else
+    prefill_mfma_kernel<false, false, true><<<grid, kThreads, 0, stream>>>(
+        query_gate, key, value, nullptr, out, cache, tokens, max_ctx, past, nq);
 }
 
 } // namespace raftinfer::amd

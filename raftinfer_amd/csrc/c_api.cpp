@@ -68,6 +68,10 @@ template <typename T> T &out_ref(T *p) {
   return *p;
 }
 RaftInferDataType to_dtype(int d) { return static_cast<RaftInferDataType>(d); }
+Qwen35FusedNormRope to_norm(raftinfer_amd_fused_norm_rope n) {
+  return {n.query_norm_weight, n.key_norm_weight, static_cast<RaftInferDataType>(n.weight_dtype),
+          n.rotary_dim, n.rope_base, n.epsilon};
+}
 
 } // namespace
 
@@ -226,11 +230,6 @@ int raftinfer_amd_online_attention_decode_partition_only(
   });
 }
 
-Qwen35FusedNormRope to_norm(raftinfer_amd_fused_norm_rope n) {
-  return {n.query_norm_weight, n.key_norm_weight, static_cast<RaftInferDataType>(n.weight_dtype),
-          n.rotary_dim, n.rope_base, n.epsilon};
-}
-
 int raftinfer_amd_online_attention_decode_fused(
     const void *qg, const void *k, const void *v, void *o, void *cache, size_t cache_bytes, void *ws,
     size_t ws_bytes, raftinfer_amd_attention_shape shape, raftinfer_amd_fused_norm_rope norm,
@@ -241,6 +240,18 @@ int raftinfer_amd_online_attention_decode_fused(
         qg, k, v, o, cache, cache_bytes, ws, ws_bytes, to_shape(shape), to_norm(norm),
         static_cast<Qwen35KvCacheDType>(cache_dtype), static_cast<Qwen35KvCacheLayout>(cache_layout),
         to_plan(plan), device_position, to_stream(stream));
+  });
+}
+
+int raftinfer_amd_online_attention_prefill_fused(
+    const void *qg, const void *k, const void *v, void *o, void *cache, size_t cache_bytes,
+    raftinfer_amd_attention_shape shape, raftinfer_amd_fused_norm_rope norm, uint8_t cache_dtype,
+    uint8_t cache_layout, void *stream) {
+  return guarded([&] {
+    qwen35_online_attention_prefill_fused(
+        qg, k, v, o, cache, cache_bytes, to_shape(shape), to_norm(norm),
+        static_cast<Qwen35KvCacheDType>(cache_dtype), static_cast<Qwen35KvCacheLayout>(cache_layout),
+        to_stream(stream));
   });
 }
 

@@ -260,6 +260,15 @@ def qwen35_online_attention_decode_fused(query_gate, key, value, output, kv_cach
         DecodePlan(*plan), pos, _stream(stream)))
 
 
+def qwen35_online_attention_prefill_fused(query_gate, key, value, output, kv_cache, shape,
+                                          norm: Qwen35FusedNormRope, cache_dtype=CACHE_BF16,
+                                          cache_layout=HEAD_MAJOR, stream=None) -> None:
+    """The q split + RMSNorm + RoPE of q and k fused into the causal gated prefill."""
+    _call(Qwen35PrimitiveError, _lib.load().raftinfer_amd_online_attention_prefill_fused(
+        _ptr(query_gate), _ptr(key), _ptr(value), _ptr(output), _ptr(kv_cache), _nbytes(kv_cache),
+        shape.c(), norm.c(), cache_dtype, cache_layout, _stream(stream)))
+
+
 def qwen35_online_attention_static_workspace_bytes() -> int:
     return int(_lib.load().raftinfer_amd_online_attention_static_workspace_bytes())
 

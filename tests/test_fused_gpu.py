@@ -100,3 +100,67 @@ def test_fused_decode_against_oracle(gpu):
     assert_bf16_close(from_dev(c["out2"]).reshape(HQ, D), bf16(want), what="fused decode")
     ck, _ = read_cache(from_dev(c["cache2"]), 1, ctx, 4096)
     assert_bf16_close(ck[ctx - 1], kb, what="appended k")
+
+
+def _prefill_case(T, past, rot, wdt, layout, seed):
+    r = rng(seed)
+    max_ctx = past + T
+    pk, pv = bf16(normal(r, past, HKV, D)), bf16(normal(r, past, HKV, D))
+    qg = bf16(normal(r, T, HQ, 2, D))
+    kraw, v = bf16(normal(r, T, HKV, D)), bf16(normal(r, T, HKV, D))
+    wq, wk = _norm_weights(r, wdt)
+    base, eps = 1e7, 1e-6
+    cache0 = to_dev(make_cache(pk, pv, layout, max_ctx), BF)
+    shape = ops.Qwen35AttentionShape(T, HQ, HKV, D, max_ctx, past)
+    dqg, dk, dv = to_dev(qg, BF), to_dev(kraw, BF), to_dev(v, BF)
+    dwq, dwk = to_dev(wq, wdt), to_dev(wk, wdt)
+    wcode = ops.DTYPE_F32 if wdt == torch.float32 else ops.DTYPE_BF16
+    q1 = torch.empty(T * HQ * D, device="cuda", dtype=BF)
+    g1 = torch.empty(T * HQ * D, device="cuda", dtype=BF)
+    k1 = torch.empty(T * HKV * D, device="cuda", dtype=BF)
+    ops.qwen35_split_query_gate_norm_rope(dqg, dwq, q1, g1, ops.QkNormRopeShape(T, HQ, D, rot, past, base),
+                                          eps, ops.DTYPE_BF16, wcode)
+    ops.qwen35_qk_norm_rope(dk, dwk, k1, ops.QkNormRopeShape(T, HKV, D, rot, past, base), eps,
+                            ops.DTYPE_BF16, wcode)
+    out1 = torch.empty(T * HQ * D, device="cuda", dtype=BF)
+    cache1 = cache0.clone()
+    ops.qwen35_causal_attention(q1, k1, dv, g1, out1, cache1, None, shape, ops.DTYPE_BF16,
+                                ops.Qwen35AttentionLaunchPolicy(1, ops.CACHE_BF16, layout))
+    out2 = torch.empty(T * HQ * D, device="cuda", dtype=BF)
+    cache2 = cache0.clone()
+    ops.qwen35_online_attention_prefill_fused(dqg, dk, dv, out2, cache2, shape,
+                                              ops.Qwen35FusedNormRope(dwq, dwk, rot, base, eps),
+                                              ops.CACHE_BF16, layout)
+    torch.cuda.synchronize()
+    return dict(out1=out1, out2=out2, cache1=cache1, cache2=cache2, qg=qg, kraw=kraw, v=v, wq=wq,
+                wk=wk, pk=pk, pv=pv)
+
+
+@pytest.mark.parametrize("T,past", [(2, 0), (7, 0), (40, 0), (128, 0), (512, 0), (17, 111), (300, 33)])
+def test_fused_prefill_equals_producers_then_attention(gpu, T, past):
+    c = _prefill_case(T, past, 64, torch.bfloat16, ops.HEAD_MAJOR, seed=T + past)
+    assert torch.equal(c["cache1"], c["cache2"])
+    assert torch.equal(c["out1"], c["out2"])
+
+
+@pytest.mark.parametrize("rot,wdt,layout", [(256, torch.float32, ops.HEAD_MAJOR),
+                                            (8, torch.bfloat16, ops.TOKEN_MAJOR),
+                                            (128, torch.float32, ops.TOKEN_MAJOR)])
+def test_fused_prefill_rotary_weights_layouts(gpu, rot, wdt, layout):
+    c = _prefill_case(70, 5, rot, wdt, layout, seed=rot + 1)
+    assert torch.equal(c["cache1"], c["cache2"])
+    assert torch.equal(c["out1"], c["out2"])
+
+
+def test_fused_prefill_against_oracle(gpu):
+    T, past, rot, base, eps = 96, 20, 64, 1e7, 1e-6
+    c = _prefill_case(T, past, rot, torch.bfloat16, ops.HEAD_MAJOR, seed=9)
+    q = bf16(orc.qk_norm_rope(c["qg"][:, :, 0], c["wq"], rot, past, base, eps))
+    k = bf16(orc.qk_norm_rope(c["kraw"], c["wk"], rot, past, base, eps))
+    keys = np.concatenate([c["pk"], k])
+    vals = np.concatenate([c["pv"], c["v"]])
+    want = orc.attention_core(q, keys, vals, c["qg"][:, :, 1], past)
+    assert_bf16_close(from_dev(c["out2"]).reshape(T, HQ, D), bf16(want), what="fused prefill")
+    ck, cv = read_cache(from_dev(c["cache2"]), 1, past + T, past + T)
+    assert_bf16_close(ck[past:], k, what="appended k")
+    assert np.array_equal(cv[past:], c["v"])
