@@ -557,6 +557,63 @@ def main():
             "split_only_us": us_s, "split_only_GB_per_s": fbytes / us_s / 1e3}
         log(f"producers PP512: fused q {us_f:.1f} us, k {us_k:.1f} us, split {us_s:.1f} us")
 
+        # ------------- whole attention steps: producers separate vs fused in
+        # PP512 prefill: q split+norm+RoPE, k norm+RoPE, prefill (3 launches)
+        # against the fused entry (2 launches); hot inputs.
+        wq32 = torch.randn(D, device="cuda") * 0.2 + 1.0
+        wk32 = torch.randn(D, device="cuda") * 0.2 + 1.0
+        wqb, wkb = wq32.to(torch.bfloat16), wk32.to(torch.bfloat16)
+        norm = ops.Qwen35FusedNormRope(wqb, wkb, 64, 1e7, 1e-6)
+        pshape = ops.Qwen35AttentionShape(T, HQ, HKV, D, T, 0)
+        vin = rand_bf16(T * HKV * D)
+        pcache = torch.zeros(2 * T * HKV * D, device="cuda", dtype=torch.bfloat16)
+        pout = torch.empty(T * HQ * D, device="cuda", dtype=torch.bfloat16)
+        pol = ops.Qwen35AttentionLaunchPolicy()
+
+        def prefill_step(i):
+            ops.qwen35_split_query_gate_norm_rope(qg, wqb, qo, go, qshape, 1e-6, 3, 3, stream=stream)
+            ops.qwen35_qk_norm_rope(kin, wkb, ko, kshape, 1e-6, 3, 3, stream=stream)
+            ops.qwen35_causal_attention(qo, ko, vin, go, pout, pcache, None, pshape, ops.DTYPE_BF16, pol,
+                                        stream=stream)
+        us_sep = timed(prefill_step, args.steps, args.warmup, cold=False)
+        us_fus = timed(lambda i: ops.qwen35_online_attention_prefill_fused(
+            qg, kin, vin, pout, pcache, pshape, norm, stream=stream), args.steps, args.warmup, cold=False)
+        # ctx 4096 decode step: producers + split-K decode (4 launches) against
+        # the fused decode (2 launches); a distinct cache per call, cold.
+        ctx = 4096
+        ncache = n_caches(ctx, args.steps)
+        caches = make_caches(ctx, ncache)
+        dshape = ops.Qwen35AttentionShape(1, HQ, HKV, D, ctx, ctx - 1)
+        dplan = ops.qwen35_online_decode_plan(dshape, ops.AUTO, ctx)
+        dws = torch.empty(ops.qwen35_online_decode_workspace_layout(dshape, dplan[0])[4], device="cuda",
+                          dtype=torch.uint8)
+        qg1, k1raw, v1 = rand_bf16(HQ * 2 * D), rand_bf16(HKV * D), rand_bf16(HKV * D)
+        q1, g1 = (torch.empty(HQ * D, device="cuda", dtype=torch.bfloat16) for _ in range(2))
+        k1 = torch.empty(HKV * D, device="cuda", dtype=torch.bfloat16)
+        o1 = torch.empty(HQ * D, device="cuda", dtype=torch.bfloat16)
+        q1s = ops.QkNormRopeShape(1, HQ, D, 64, ctx - 1, 1e7)
+        k1s = ops.QkNormRopeShape(1, HKV, D, 64, ctx - 1, 1e7)
+
+        def decode_step(i):
+            ops.qwen35_split_query_gate_norm_rope(qg1, wqb, q1, g1, q1s, 1e-6, 3, 3, stream=stream)
+            ops.qwen35_qk_norm_rope(k1raw, wkb, k1, k1s, 1e-6, 3, 3, stream=stream)
+            ops.qwen35_online_attention_decode(q1, k1, v1, g1, o1, caches[i % ncache], dws, dshape,
+                                               ops.DTYPE_BF16, ops.CACHE_BF16, ops.HEAD_MAJOR, plan=dplan,
+                                               stream=stream)
+        ud_sep = timed(decode_step, args.steps, args.warmup, cold=True)
+        ud_fus = timed(lambda i: ops.qwen35_online_attention_decode_fused(
+            qg1, k1raw, v1, o1, caches[i % ncache], dws, dshape, norm, ops.CACHE_BF16, ops.HEAD_MAJOR,
+            dplan, stream=stream), args.steps, args.warmup, cold=True)
+        del caches
+        torch.cuda.empty_cache()
+        results["fused_producers"] = {
+            "prefill_pp512_separate_us": us_sep, "prefill_pp512_fused_us": us_fus,
+            "decode_ctx4096_separate_us": ud_sep, "decode_ctx4096_fused_us": ud_fus,
+            "note": "separate = q split+norm+RoPE, k norm+RoPE, then attention; fused = the producers "
+                    "inside the attention kernels (bit-identical results)"}
+        log(f"attention step with producers: PP512 {us_sep:.1f} -> {us_fus:.1f} us fused; "
+            f"decode ctx4096 {ud_sep:.1f} -> {ud_fus:.1f} us fused")
+
     # ------------------------------------------------------ CPU baseline
     cpu = None
     if not args.no_cpu:
