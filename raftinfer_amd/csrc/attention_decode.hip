@@ -477,21 +477,19 @@ __device__ __forceinline__ void append_rows_fused(const DecodeMfmaArgs &a, const
 
 // gate: element (head h, dim d) at gate[h * gate_stride + d] (gate_stride 256
 // for a split gate, 512 for the gate half of a q projection row).
-template <int DS, int WAVES, bool kFused = false>
-__global__ __launch_bounds__(WAVES * 64) void decode_single_mfma_kernel(
-    DecodeMfmaArgs a, const bf16_bits *__restrict__ gate, std::size_t gate_stride,
-    bf16_bits *__restrict__ output, std::size_t host_position, const std::uint32_t *device_position,
-    std::size_t threshold, FusedNormRope f) {
-  __shared__ DecodeMfmaShared<DS, WAVES> sh;
-  __shared__ DecodeFusedQK fq;
+// Single-block workgroup `block` at `position` (ctx = position + 1).
+template <int DS, int WAVES, bool kFused>
+__device__ __forceinline__ void single_block_body(unsigned block, const DecodeMfmaArgs &a,
+                                                  const bf16_bits *__restrict__ gate,
+                                                  std::size_t gate_stride,
+                                                  bf16_bits *__restrict__ output,
+                                                  std::size_t position, const FusedNormRope &f,
+                                                  DecodeMfmaShared<DS, WAVES> &sh, DecodeFusedQK &fq) {
   constexpr int DIMS = kHeadDim / DS;
-  const std::size_t position = read_position(device_position, host_position);
-  if (position >= a.max_ctx) return;
   const std::size_t ctx = position + 1;
-  if (threshold != 0 && ctx >= threshold) return;
   std::size_t kv_head;
   int dq;
-  xcd_unit<DS>(blockIdx.x, kv_head, dq);
+  xcd_unit<DS>(block, kv_head, dq);
   if (kv_head >= kKvHeads) return;
   // The gate values of this thread's outputs are loaded before the scan, so
   // the epilogue does not wait for a load round trip of its own.
@@ -527,22 +525,32 @@ __global__ __launch_bounds__(WAVES * 64) void decode_single_mfma_kernel(
   }
 }
 
-template <int DS, int WAVES, int CT = 32, bool kFused = false>
-__global__ __launch_bounds__(WAVES * 64) void decode_split_mfma_kernel(
-    DecodeMfmaArgs a, float *__restrict__ pmax, float *__restrict__ psum,
-    float *__restrict__ pval, std::size_t host_position, const std::uint32_t *device_position,
-    std::size_t capacity, std::size_t max_partitions, std::size_t partition_tokens,
+template <int DS, int WAVES, bool kFused = false>
+__global__ __launch_bounds__(WAVES * 64) void decode_single_mfma_kernel(
+    DecodeMfmaArgs a, const bf16_bits *__restrict__ gate, std::size_t gate_stride,
+    bf16_bits *__restrict__ output, std::size_t host_position, const std::uint32_t *device_position,
     std::size_t threshold, FusedNormRope f) {
-  __shared__ DecodeMfmaShared<DS, WAVES, CT> sh;
+  __shared__ DecodeMfmaShared<DS, WAVES> sh;
   __shared__ DecodeFusedQK fq;
-  constexpr int DIMS = kHeadDim / DS;
   const std::size_t position = read_position(device_position, host_position);
   if (position >= a.max_ctx) return;
+  if (threshold != 0 && position + 1 >= threshold) return;
+  single_block_body<DS, WAVES, kFused>(blockIdx.x, a, gate, gate_stride, output, position, f, sh, fq);
+}
+
+// Split-K partition workgroup `block` at `position`.
+template <int DS, int WAVES, int CT, bool kFused>
+__device__ __forceinline__ void split_body(unsigned block, const DecodeMfmaArgs &a,
+                                           float *__restrict__ pmax, float *__restrict__ psum,
+                                           float *__restrict__ pval, std::size_t position,
+                                           std::size_t capacity, std::size_t max_partitions,
+                                           std::size_t partition_tokens, const FusedNormRope &f,
+                                           DecodeMfmaShared<DS, WAVES, CT> &sh, DecodeFusedQK &fq) {
+  constexpr int DIMS = kHeadDim / DS;
   const std::size_t ctx = position + 1;
-  if (ctx < threshold) return;
   std::size_t unit;
   int dq;
-  xcd_unit<DS>(blockIdx.x, unit, dq);
+  xcd_unit<DS>(block, unit, dq);
   if (unit >= kKvHeads * capacity) return;
   const std::size_t kv_head = unit / capacity;
   const std::size_t partition = unit % capacity;
@@ -578,6 +586,46 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_mfma_kernel(
   }
 }
 
+template <int DS, int WAVES, int CT = 32, bool kFused = false>
+__global__ __launch_bounds__(WAVES * 64) void decode_split_mfma_kernel(
+    DecodeMfmaArgs a, float *__restrict__ pmax, float *__restrict__ psum,
+    float *__restrict__ pval, std::size_t host_position, const std::uint32_t *device_position,
+    std::size_t capacity, std::size_t max_partitions, std::size_t partition_tokens,
+    std::size_t threshold, FusedNormRope f) {
+  __shared__ DecodeMfmaShared<DS, WAVES, CT> sh;
+  __shared__ DecodeFusedQK fq;
+  const std::size_t position = read_position(device_position, host_position);
+  if (position >= a.max_ctx) return;
+  if (position + 1 < threshold) return;
+  split_body<DS, WAVES, CT, kFused>(blockIdx.x, a, pmax, psum, pval, position, capacity,
+                                    max_partitions, partition_tokens, f, sh, fq);
+}
+
+// Device-position decode of a split-K plan in one launch instead of two: the
+// position is read on the device, and below the split threshold the first
+// blocks run the single-block scan (writing the gated output) while the rest
+// exit; from the threshold on the grid runs the split-K partitions.  The
+// merge kernel that follows exits below the threshold, as before.
+template <int DS, int WAVES, bool kFused>
+__global__ __launch_bounds__(WAVES * 64) void decode_dynamic_mfma_kernel(
+    DecodeMfmaArgs a, const bf16_bits *__restrict__ gate, std::size_t gate_stride,
+    bf16_bits *__restrict__ output, float *__restrict__ pmax, float *__restrict__ psum,
+    float *__restrict__ pval, const std::uint32_t *device_position, std::size_t capacity,
+    std::size_t max_partitions, std::size_t partition_tokens, std::size_t threshold,
+    FusedNormRope f) {
+  __shared__ DecodeMfmaShared<kSingleDs, WAVES> ssh;
+  __shared__ DecodeMfmaShared<DS, WAVES, 32> psh;
+  __shared__ DecodeFusedQK fq;
+  const std::size_t position = *device_position;
+  if (position >= a.max_ctx) return;
+  if (position + 1 < threshold)
+    single_block_body<kSingleDs, WAVES, kFused>(blockIdx.x, a, gate, gate_stride, output, position, f,
+                                                ssh, fq);
+  else
+    split_body<DS, WAVES, 32, kFused>(blockIdx.x, a, pmax, psum, pval, position, capacity,
+                                      max_partitions, partition_tokens, f, psh, fq);
+}
+
 // ------------------------------------------------------------ launchers
 
 // Plans of at most 16 partitions (ctx 4096 at P=256) use the 64-workgroup
@@ -600,6 +648,47 @@ void launch_merge(const ActT *g, std::size_t gate_stride, ActT *out, const float
         max_partitions, plan.active_partition_capacity, plan.split_k_threshold_tokens, device_position);
 }
 
+// Device-position decode of a split-K plan: decode_dynamic_mfma_kernel (the
+// single-block or the partition work, chosen on the device), then the merge.
+template <bool kFused>
+void launch_dynamic_decode(const DecodeMfmaArgs &args, const bf16_bits *g, std::size_t gate_stride,
+                           bf16_bits *out, void *workspace, Qwen35AttentionShape shape,
+                           Qwen35OnlineDecodePlan plan, Qwen35OnlineDecodeWorkspaceLayout ws,
+                           const std::uint32_t *device_position, hipStream_t stream,
+                           FusedNormRope f) {
+  const std::size_t max_partitions = ceil_div(shape.max_context_tokens, plan.partition_tokens,
+                                              "online decode maximum partition capacity overflow");
+  const std::size_t units = checked_mul<Err>(kKvHeads, plan.active_partition_capacity,
+                                             "online decode partition grid dimension overflow");
+  (void)grid_dim(checked_mul<Err>(units + 8, kSplitDs, "online decode partition grid dimension overflow"),
+                 "online decode partition grid dimension overflow");
+  auto *bytes = static_cast<std::byte *>(workspace);
+  auto *pmax = reinterpret_cast<float *>(bytes + ws.max_offset_bytes);
+  auto *psum = reinterpret_cast<float *>(bytes + ws.sum_offset_bytes);
+  auto *pval = reinterpret_cast<float *>(bytes + ws.value_offset_bytes);
+  const unsigned single_grid = xcd_grid<kSingleDs>(kKvHeads);
+  auto grid_for = [&](unsigned split_grid) { return split_grid > single_grid ? split_grid : single_grid; };
+  if (units >= 192)
+    decode_dynamic_mfma_kernel<1, kSplitWaves, kFused><<<grid_for(xcd_grid<1>(units)), kSplitWaves * 64, 0, stream>>>(
+        args, g, gate_stride, out, pmax, psum, pval, device_position, plan.active_partition_capacity,
+        max_partitions, plan.partition_tokens, plan.split_k_threshold_tokens, f);
+  else if (units >= 96)
+    decode_dynamic_mfma_kernel<2, kSplitWaves, kFused><<<grid_for(xcd_grid<2>(units)), kSplitWaves * 64, 0, stream>>>(
+        args, g, gate_stride, out, pmax, psum, pval, device_position, plan.active_partition_capacity,
+        max_partitions, plan.partition_tokens, plan.split_k_threshold_tokens, f);
+  else
+    decode_dynamic_mfma_kernel<kSplitDs, kSplitWaves, kFused>
+        <<<grid_for(xcd_grid<kSplitDs>(units)), kSplitWaves * 64, 0, stream>>>(
+            args, g, gate_stride, out, pmax, psum, pval, device_position, plan.active_partition_capacity,
+            max_partitions, plan.partition_tokens, plan.split_k_threshold_tokens, f);
+  check_launch<Err>(plan.partition_tokens == 256
+                        ? "qwen35_online_attention_decode_split_k_256_partition"
+                        : "qwen35_online_attention_decode_split_k_512_partition");
+  launch_merge<bf16_bits>(g, gate_stride, out, pmax, psum, pval, shape, plan, max_partitions,
+                          device_position, stream);
+  check_launch<Err>("qwen35_online_attention_decode_split_k_merge");
+}
+
 // bf16 activations and cache: single-block and / or split-K MFMA kernels of
 // the plan, then the merge.  kFused: q and k are normalised and rotated in
 // the kernels (fused producers) and the gate is the q projection's second half.
@@ -613,6 +702,12 @@ void launch_decode_mfma(const DecodeMfmaArgs &args, const bf16_bits *g, std::siz
   const bool dynamic = device_position != nullptr;
   const bool single = plan.resolved_mode == Qwen35DecodeAttentionMode::single_block;
   if (partition_only) require<Err>(!single, "partition-only decode needs a split-K plan");
+  if (dynamic && !single && !partition_only) {
+    // one launch selects single-block or split-K on the device, then the merge
+    launch_dynamic_decode<kFused>(args, g, gate_stride, out, workspace, shape, plan, ws,
+                                  device_position, stream, f);
+    return;
+  }
   if (!partition_only && (dynamic || single || host_ctx < plan.split_k_threshold_tokens)) {
     decode_single_mfma_kernel<kSingleDs, kSingleMfmaWaves, kFused>
         <<<xcd_grid<kSingleDs>(kKvHeads), kSingleMfmaWaves * 64, 0, stream>>>(
