@@ -21,6 +21,10 @@
 //                         D = U - W S, O = e^G (Q S) + M D,
 //                         S' = e^{G_last} S + (e^{G_last-G} K)^T D.
 //                         Only differences G_i - G_j <= 0 are exponentiated.
+//      chunk_tb_kernel    the same recurrence for bf16 q / k / v (the
+//      + chunk_tscan_kernel core entry): the record holds only T diag(beta)
+//                         and M, and the scan forms D = T diag(beta) (V -
+//                         e^G K S) from the inputs.
 //   3. out_norm_kernel    RMSNorm(raw) * w * SiLU(z) -> activation dtype.
 // Host validation mirrors cpp/kernels/qwen35_delta.cu:26-135, :761-897.
 #include "common.hpp"
@@ -56,11 +60,21 @@ constexpr std::size_t kG = kU + kChunk * kChunkDim * 4;              // f32  [64
 constexpr std::size_t kBytes = kG + kChunk * 4;                      // 147,712
 } // namespace rec
 
+// Records of the bf16-input path (q, k, v exact in bf16): the scan reads Q,
+// K and V from the inputs; the record holds the chunk's two 64 x 64 factors.
+namespace rec2 {
+constexpr std::size_t kTb = 0;                            // bf16 [2][64][64]  T diag(beta) (hi, lo)
+constexpr std::size_t kM = kTb + 2 * kChunk * kChunk * 2; // bf16 [2][64][64]  M (hi, lo)
+constexpr std::size_t kG = kM + 2 * kChunk * kChunk * 2;  // f32  [64]        G (padded with G[L-1])
+constexpr std::size_t kBytes = kG + kChunk * 4;           // 33,024
+} // namespace rec2
+
 struct ChunkScratch {
-  unsigned char *rec; // [hv][chunks] records of rec::kBytes
+  unsigned char *rec; // [hv][chunks] records of `bytes` (rec::kBytes or rec2::kBytes)
   std::size_t chunks;
+  std::size_t bytes;
   __device__ __forceinline__ unsigned char *at(std::size_t h, std::size_t c) const {
-    return rec + (h * chunks + c) * rec::kBytes;
+    return rec + (h * chunks + c) * bytes;
   }
 };
 
@@ -69,11 +83,12 @@ std::size_t record_offset(std::size_t per_token_bytes) {
   return checked_add<Err>(per_token_bytes, 255, "gated-delta workspace byte size overflow") & ~std::size_t{255};
 }
 
-std::size_t chunk_record_bytes(std::size_t tokens, std::size_t hv, std::size_t dk, std::size_t dv) {
+std::size_t chunk_record_bytes(std::size_t tokens, std::size_t hv, std::size_t dk, std::size_t dv,
+                               std::size_t record = rec::kBytes) {
   if (dk != kChunkDim || dv != kChunkDim) return 0;
   return checked_mul<Err>(checked_mul<Err>(hv, ceil_div_unchecked(tokens, kChunk),
                                            "gated-delta workspace shape overflow"),
-                          rec::kBytes, "gated-delta workspace shape overflow");
+                          record, "gated-delta workspace shape overflow");
 }
 
 struct CheckedShape {
@@ -1053,16 +1068,6 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
   }
   kb.store(sh.k, ks.scale);
   qb.store(sh.qv, qs.scale);
-  if constexpr (std::is_same_v<InT, bf16_bits>) {
-    // bf16 inputs are exact in bf16: the record keeps them unscaled (hi part
-    // only) and the scan applies q_scale / k_scale to its products.
-    bf16_bits *qr = reinterpret_cast<bf16_bits *>(record + rec::kQ);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int p = tid + 256 * r;
-      *reinterpret_cast<u32x4 *>(qr + (p >> 4) * kChunkDim + 8 * (p & 15)) = qb.c[r].w;
-    }
-  }
   RowBlock<InT> vb; // issued now, consumed after the Q-dependent products
   vb.load(L, [&](int i, int d) { return src_row(vs, t0 + i, h, d); });
   if (tid < kChunk) {
@@ -1093,21 +1098,17 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
       sh.a[i][j] = (j < i && i < L) ? sh.beta[i] * e * aa[r] : 0.f;
     }
   }
-  // Q and K^T go to the record before Q's LDS is reused: fp32 inputs as
-  // (Q * q_scale, (K * k_scale)^T) split pairs, bf16 inputs unscaled.
-  constexpr bool kExact = std::is_same_v<InT, bf16_bits>;
-  if constexpr (!kExact)
-    write_split_rows<kLd>(sh.qv, kChunk, kChunkDim, reinterpret_cast<bf16_bits *>(record + rec::kQ));
+  // Q and K^T go to the record before Q's LDS is reused, as
+  // (Q * q_scale, (K * k_scale)^T) split pairs.
+  write_split_rows<kLd>(sh.qv, kChunk, kChunkDim, reinterpret_cast<bf16_bits *>(record + rec::kQ));
   {
     bf16_bits *kt = reinterpret_cast<bf16_bits *>(record + rec::kKt);
-    const float kinv = kExact ? 1.0f / ks.scale : 1.0f;
     for (int item = tid; item < kChunkDim * (kChunk / 2); item += 256) {
       const int d = item / (kChunk / 2), j = 2 * (item % (kChunk / 2));
       std::uint32_t hi, lo;
-      split2(sh.k[j][d] * kinv, sh.k[j + 1][d] * kinv, hi, lo);
+      split2(sh.k[j][d], sh.k[j + 1][d], hi, lo);
       *reinterpret_cast<std::uint32_t *>(kt + d * kChunk + j) = hi;
-      if constexpr (!kExact)
-        *reinterpret_cast<std::uint32_t *>(kt + kChunkDim * kChunk + d * kChunk + j) = lo;
+      *reinterpret_cast<std::uint32_t *>(kt + kChunkDim * kChunk + d * kChunk + j) = lo;
     }
   }
   __syncthreads();
@@ -1157,255 +1158,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
   if (tid < kChunk) reinterpret_cast<float *>(record + rec::kG)[tid] = sh.g[tid];
 }
 
-// bf16 (exact) inputs: the same chunk quantities on bf16 MFMA.  q.k and k.k
-// are exact bf16 products with fp32 accumulation; the T-weighted sums
-// W = T diag(beta e^G) K and U = T diag(beta) V take the fp32 left factor as a
-// (hi, lo) split, two MFMAs per k-step.  The record holds Q and K^T unscaled.
-constexpr int kPrepThreads = 512; // bf16 chunk prep: 8 waves, two per SIMD
-
-struct PrepBShared {
-  union {
-    struct {
-      bf16_bits q[kChunk][kChunkDim + 8];
-      bf16_bits k[kChunk][kChunkDim + 8];
-    } qk;
-    float w[kChunk][kLd]; // W staging
-    float y[32][36];      // inverse scratch (Q, K no longer needed then)
-  } r1;
-  bf16_bits kt[kChunkDim][kChunk + 8]; // K^T [d][j]
-  bf16_bits vt[kChunkDim][kChunk + 8]; // V^T [d][j]
-  union {
-    struct {
-      float a[kChunk][kLdC];
-      float tm[kChunk][kLdC];
-    } at;
-    float u[kChunk][kLd]; // U staging
-  } r3;
-  float mm[kChunk][kLdC];
-  bf16_bits tw[2][kChunk][kChunk + 8]; // T diag(beta e^G k_scale), split
-  bf16_bits tu[2][kChunk][kChunk + 8]; // T diag(beta v_scale), split
-  float g[kChunk];
-  float beta[kChunk];
-};
-
 __device__ __forceinline__ bf16x8 lds8(const bf16_bits *p) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(p));
-}
-__device__ __forceinline__ floatx4 mfma_b(const bf16_bits *a, const bf16_bits *b, floatx4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-      __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(a)),
-      __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(b)), c, 0, 0, 0);
-}
-
-__global__ __launch_bounds__(kPrepThreads) void chunk_prep_bf16_kernel(Src<bf16_bits> qs, Src<bf16_bits> ks,
-                                                              Src<bf16_bits> vs,
-                                                              const float *__restrict__ beta,
-                                                              const float *__restrict__ gdecay,
-                                                              ChunkScratch scratch,
-                                                              std::size_t tokens, std::size_t hk,
-                                                              std::size_t hv) {
-  __shared__ PrepBShared sh;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int lr = lane & 15, lk = lane >> 4;
-  const std::size_t h = blockIdx.x;
-  const std::size_t kh = h % hk;
-  const std::size_t t0 = static_cast<std::size_t>(blockIdx.y) * kChunk;
-  const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
-  unsigned char *record = scratch.at(h, blockIdx.y);
-
-  // Q rows: item (tid + 512 r) -> row item / 16, dims 8 (item % 16) .. +7.
-  // K and V: thread -> token pair 2 (tid % 32) + {0, 1}, dims 8 (tid / 32)
-  // .. +7, so the transposed tiles are written straight from registers, one
-  // dword (two tokens) per store.  Rows past L repeat row L-1.
-  u32x4 qv[2];
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int p = tid + kPrepThreads * r, i = p >> 4, d = 8 * (p & 15);
-    qv[r] = *reinterpret_cast<const u32x4 *>(src_row(qs, t0 + (i < L ? i : L - 1), kh, d));
-  }
-  Chunk8<bf16_bits> kp[2], vp[2];
-  const int j0 = 2 * (tid & 31), dkv = 8 * (tid >> 5);
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int j = j0 + e < L ? j0 + e : L - 1;
-    kp[e].w = *reinterpret_cast<const u32x4 *>(src_row(ks, t0 + j, kh, dkv));
-    vp[e].w = *reinterpret_cast<const u32x4 *>(src_row(vs, t0 + j, h, dkv));
-  }
-  float bt = 0.f, gt = 0.f;
-  if (tid < L) {
-    bt = beta[(t0 + tid) * hv + h];
-    gt = gdecay[(t0 + tid) * hv + h];
-  }
-  bf16_bits *qrec = reinterpret_cast<bf16_bits *>(record + rec::kQ);
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int p = tid + kPrepThreads * r, i = p >> 4, d = 8 * (p & 15);
-    *reinterpret_cast<u32x4 *>(&sh.r1.qk.q[i][d]) = qv[r];
-    *reinterpret_cast<u32x4 *>(qrec + i * kChunkDim + d) = qv[r];
-  }
-  *reinterpret_cast<u32x4 *>(&sh.r1.qk.k[j0][dkv]) = kp[0].w;
-  *reinterpret_cast<u32x4 *>(&sh.r1.qk.k[j0 + 1][dkv]) = kp[1].w;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int sh16 = 16 * (e & 1);
-    const std::uint32_t k0 = (kp[0].w[e >> 1] >> sh16) & 0xFFFFu, k1 = (kp[1].w[e >> 1] >> sh16) & 0xFFFFu;
-    const std::uint32_t v0 = (vp[0].w[e >> 1] >> sh16) & 0xFFFFu, v1 = (vp[1].w[e >> 1] >> sh16) & 0xFFFFu;
-    *reinterpret_cast<std::uint32_t *>(&sh.kt[dkv + e][j0]) = k0 | (k1 << 16);
-    *reinterpret_cast<std::uint32_t *>(&sh.vt[dkv + e][j0]) = v0 | (v1 << 16);
-  }
-  if (tid < kChunk) {
-    sh.beta[tid] = bt;
-    sh.g[tid] = gt;
-  }
-  __syncthreads();
-  if (wave == 0) sh.g[lane] = wave_prefix_sum(sh.g[lane]); // rows past L repeat G[L-1] (g = 0)
-  __syncthreads();
-  {
-    bf16_bits *kr = reinterpret_cast<bf16_bits *>(record + rec::kKt);
-    u32x4 kv[2];
-#pragma unroll
-    for (int n = 0; n < 2; ++n) {
-      const int item = tid + kPrepThreads * n, d = item >> 3, j = 8 * (item & 7);
-      kv[n] = *reinterpret_cast<const u32x4 *>(&sh.kt[d][j]);
-    }
-#pragma unroll
-    for (int n = 0; n < 2; ++n) {
-      const int item = tid + kPrepThreads * n, d = item >> 3, j = 8 * (item & 7);
-      *reinterpret_cast<u32x4 *>(kr + d * kChunk + j) = kv[n];
-    }
-  }
-  // M = e^{G_i-G_j} (q_i . k_j) q_scale k_scale (j <= i), A = beta_i e^{G_i-G_j}
-  // (k_i . k_j) k_scale^2 (j < i), exact bf16 products.  Wave w takes row
-  // tile ti = w % 4 and column tiles tj = 2 (w / 4) + {0, 1}; tiles above the
-  // diagonal are written as 0 without products.
-  const float qk_scale = qs.scale * ks.scale, kk_scale = ks.scale * ks.scale;
-  {
-    const int ti = wave & 3, tj0 = 2 * (wave >> 2);
-    // Per-lane decay and beta values, read once: rows i = 16 ti + 4 lk + r,
-    // columns j = 16 tj + lr.
-    float gi[4], bi[4], gj[2];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      gi[r] = sh.g[ti * 16 + lk * 4 + r];
-      bi[r] = sh.beta[ti * 16 + lk * 4 + r] * kk_scale;
-    }
-#pragma unroll
-    for (int n = 0; n < 2; ++n) gj[n] = sh.g[(tj0 + n) * 16 + lr];
-    // Operands are read before the products, and every product runs before
-    // any result is scaled, so LDS latency is paid about once.
-    bf16x8 qrow[4], krow[4];
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      qrow[kk] = lds8(&sh.r1.qk.q[ti * 16 + lr][32 * kk + 8 * lk]);
-      krow[kk] = lds8(&sh.r1.qk.k[ti * 16 + lr][32 * kk + 8 * lk]);
-    }
-    floatx4 am[2], aa[2];
-#pragma unroll
-    for (int n = 0; n < 2; ++n) {
-      am[n] = floatx4{};
-      aa[n] = floatx4{};
-      if (tj0 + n <= ti) {
-        bf16x8 kcol[4];
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) kcol[kk] = lds8(&sh.r1.qk.k[(tj0 + n) * 16 + lr][32 * kk + 8 * lk]);
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          am[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qrow[kk], kcol[kk], am[n], 0, 0, 0);
-          aa[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(krow[kk], kcol[kk], aa[n], 0, 0, 0);
-        }
-      }
-    }
-#pragma unroll
-    for (int n = 0; n < 2; ++n) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = ti * 16 + lk * 4 + r, j = (tj0 + n) * 16 + lr;
-        const float e = __expf(gi[r] - gj[n]);
-        sh.mm[i][j] = (j <= i && i < L) ? am[n][r] * qk_scale * e : 0.f;
-        sh.r3.at.a[i][j] = (j < i && i < L) ? bi[r] * e * aa[n][r] : 0.f;
-      }
-    }
-  }
-  __syncthreads();
-  invert_unit_lower_64(sh.r3.at.a, sh.r3.at.tm, sh.r1.y);
-  // tw = T diag(beta e^G k_scale), tu = T diag(beta v_scale), split.
-  // Thread -> column pair j = 2 (tid % 32), rows tid / 32 + 16 n: the column
-  // factors are read once and the four row pairs in one batch.
-  {
-    const int j = 2 * (tid & 31), i0 = tid >> 5;
-    const float b0 = sh.beta[j], b1 = sh.beta[j + 1];
-    const float fw0 = b0 * __expf(sh.g[j]) * ks.scale, fw1 = b1 * __expf(sh.g[j + 1]) * ks.scale;
-    const float fu0 = b0 * vs.scale, fu1 = b1 * vs.scale;
-    float2 tv[4];
-#pragma unroll
-    for (int n = 0; n < 4; ++n) tv[n] = *reinterpret_cast<const float2 *>(&sh.r3.at.tm[i0 + 16 * n][j]);
-#pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      const int i = i0 + 16 * n;
-      std::uint32_t hi, lo;
-      split2(tv[n].x * fw0, tv[n].y * fw1, hi, lo);
-      *reinterpret_cast<std::uint32_t *>(&sh.tw[0][i][j]) = hi;
-      *reinterpret_cast<std::uint32_t *>(&sh.tw[1][i][j]) = lo;
-      split2(tv[n].x * fu0, tv[n].y * fu1, hi, lo);
-      *reinterpret_cast<std::uint32_t *>(&sh.tu[0][i][j]) = hi;
-      *reinterpret_cast<std::uint32_t *>(&sh.tu[1][i][j]) = lo;
-    }
-  }
-  __syncthreads();
-  // W = tw K, U = tu V (B operands K^T, V^T): 4 x 8 tiles (ti, tn); wave w
-  // takes tn = w and ti = 0..3, so its K^T and V^T operands are read once and
-  // each row tile's operands before its eight products.
-  floatx4 aw[4], au[4];
-  {
-    bf16x8 kc[2], vc[2];
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      kc[jj] = lds8(&sh.kt[wave * 16 + lr][32 * jj + 8 * lk]);
-      vc[jj] = lds8(&sh.vt[wave * 16 + lr][32 * jj + 8 * lk]);
-    }
-#pragma unroll
-    for (int ti = 0; ti < 4; ++ti) {
-      bf16x8 w0[2], w1[2], u0[2], u1[2];
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const int ja = 32 * jj + 8 * lk;
-        w0[jj] = lds8(&sh.tw[0][ti * 16 + lr][ja]);
-        w1[jj] = lds8(&sh.tw[1][ti * 16 + lr][ja]);
-        u0[jj] = lds8(&sh.tu[0][ti * 16 + lr][ja]);
-        u1[jj] = lds8(&sh.tu[1][ti * 16 + lr][ja]);
-      }
-      aw[ti] = floatx4{};
-      au[ti] = floatx4{};
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        aw[ti] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0[jj], kc[jj], aw[ti], 0, 0, 0);
-        au[ti] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(u0[jj], vc[jj], au[ti], 0, 0, 0);
-        aw[ti] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1[jj], kc[jj], aw[ti], 0, 0, 0);
-        au[ti] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(u1[jj], vc[jj], au[ti], 0, 0, 0);
-      }
-    }
-  }
-  __syncthreads(); // q/k and a/tm no longer needed: stage W and U
-#pragma unroll
-  for (int ti = 0; ti < 4; ++ti) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      sh.r1.w[ti * 16 + lk * 4 + r][wave * 16 + lr] = aw[ti][r];
-      sh.r3.u[ti * 16 + lk * 4 + r][wave * 16 + lr] = au[ti][r];
-    }
-  }
-  __syncthreads();
-  write_split_rows<kLd, kPrepThreads>(sh.r1.w, kChunk, kChunkDim, reinterpret_cast<bf16_bits *>(record + rec::kW));
-  write_split_rows<kLdC, kPrepThreads>(sh.mm, kChunk, kChunk, reinterpret_cast<bf16_bits *>(record + rec::kM));
-  {
-    float *u = reinterpret_cast<float *>(record + rec::kU);
-    for (int item = tid; item < kChunk * (kChunkDim / 4); item += kPrepThreads) {
-      const int r = item / (kChunkDim / 4), c = 4 * (item % (kChunkDim / 4));
-      *reinterpret_cast<float4 *>(u + r * kChunkDim + c) =
-          make_float4(sh.r3.u[r][c], sh.r3.u[r][c + 1], sh.r3.u[r][c + 2], sh.r3.u[r][c + 3]);
-    }
-  }
-  if (tid < kChunk) reinterpret_cast<float *>(record + rec::kG)[tid] = sh.g[tid];
 }
 
 // Chunk scan on bf16 MFMA with fp32-accurate products.  The records hold
@@ -1488,8 +1242,8 @@ __device__ __forceinline__ void store_split_t(bf16_bits (*hi)[LD], bf16_bits (*l
 // Loads of chunk record `record`, in the order the scan consumes them, each
 // wave fetching only the rows it reads.  The first part (W, U, G) has
 // kFirstLoads instructions per wave, K^T kKtLoads, Q and M kQmLoads.
-template <bool kExact> struct ScanLoads {
-  static constexpr int kQkHalves = kExact ? 1 : 2; // bf16 q / k inputs have no low part
+struct ScanLoads {
+  static constexpr int kQkHalves = 2;
   static constexpr int kFirstLoads = 8 + 1 + 1;
   static constexpr int kKtLoads = 4 * kQkHalves;
   static constexpr int kQmLoads = 4 * kQkHalves + 4;
@@ -1521,13 +1275,12 @@ template <bool kExact> struct ScanLoads {
 // next chunk's record streams into LDS behind the current chunk's work: each
 // part is reissued as soon as its wave has finished reading the current one
 // (W, U, G after D; K^T after the S update; Q, M after O).
-template <bool kExact, typename OutT>
+template <typename OutT>
 __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
                                                          float *__restrict__ state,
                                                          OutT *__restrict__ out, std::size_t tokens,
-                                                         std::size_t hv, float q_scale,
-                                                         float k_scale) {
-  using Loads = ScanLoads<kExact>;
+                                                         std::size_t hv) {
+  using Loads = ScanLoads;
   __shared__ Scan3Shared sh;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1566,7 +1319,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
     const float glast = g[kChunk - 1]; // = G[L-1] (padded)
     // Per-row factors of this lane's rows i = i0 + 4 lk + r, computed before
     // the products so the exponentials overlap the MFMA latency:
-    // e^{G_last - G_i} for D~ (0 past L) and e^{G_i} q_scale for O.
+    // e^{G_last - G_i} for D~ (0 past L) and e^{G_i} for O.
     floatx4 u, fdec, eq;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -1574,7 +1327,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
       const float gi = g[i];
       u[r] = sh.u[i][lr];
       fdec[r] = i < L ? __expf(glast - gi) : 0.f;
-      eq[r] = __expf(gi) * q_scale;
+      eq[r] = __expf(gi);
     }
     // D = U - W S for rows i0 .. i0+15 (S^T is the B operand), and
     // D~ = e^{G_last - G} D for the S update (rows past L get weight 0).
@@ -1624,7 +1377,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
       for (int n = 0; n < 2; ++n) {
         const int ja = 32 * n + 8 * lk, ka = swz64(d0 + lr, 4 * n + lk);
         kh[n] = lds8(kt_hi + ka);
-        if constexpr (!kExact) kl[n] = lds8(kt_lo + ka);
+        kl[n] = lds8(kt_lo + ka);
         fh[n] = lds8(&sh.ft[0][lr][ja]);
         fl[n] = lds8(&sh.ft[1][lr][ja]);
       }
@@ -1633,13 +1386,13 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
       for (int n = 0; n < 2; ++n) {
         s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh[n], fh[n], s0, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh[n], fl[n], s1, 0, 0, 0);
-        if constexpr (!kExact) s2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl[n], fh[n], s2, 0, 0, 0);
+        s2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl[n], fh[n], s2, 0, 0, 0);
       }
       floatx4 acc;
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[r] = s0[r] + (s1[r] + s2[r]);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s[tt][r] = fmaf(egl, s[tt][r], k_scale * acc[r]);
+      for (int r = 0; r < 4; ++r) s[tt][r] = fmaf(egl, s[tt][r], acc[r]);
     }
     wait_lgkm0(); // this wave's reads of K^T are done
     if (more) {
@@ -1648,14 +1401,14 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
     } else {
       wait_vm<0>();
     }
-    // O = e^G (Q S) + M D for rows i0 .. i0+15 (q_scale is 1 unless Q is raw bf16).
+    // O = e^G (Q S) + M D for rows i0 .. i0+15.
     {
       bf16x8 qh[4], ql[4], sth[4], stl[4], mh[2], ml[2], dth[2], dtl[2];
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
         const int ka = 32 * n + 8 * lk, qo = swz128(i0 + lr, 4 * n + lk);
         qh[n] = lds8(q_hi + qo);
-        if constexpr (!kExact) ql[n] = lds8(q_lo + qo);
+        ql[n] = lds8(q_lo + qo);
         sth[n] = lds8(&sh.st[0][lr][ka]);
         stl[n] = lds8(&sh.st[1][lr][ka]);
       }
@@ -1672,7 +1425,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
       for (int n = 0; n < 4; ++n) {
         q0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh[n], sth[n], q0, 0, 0, 0);
         q1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh[n], stl[n], q1, 0, 0, 0);
-        if constexpr (!kExact) q2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql[n], sth[n], q2, 0, 0, 0);
+        q2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql[n], sth[n], q2, 0, 0, 0);
       }
 #pragma unroll
       for (int n = 0; n < 2; ++n) {
@@ -1703,6 +1456,373 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
   for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) sg[(32 * wave + 16 * tt + 4 * lk + r) * kChunkDim + c0 + lr] = s[tt][r];
+}
+
+// ------------------------------------- stage 2b, bf16 inputs: T records
+// With q, k and v exact in bf16 the scan takes Q, K and V straight from the
+// inputs, and the per-chunk record holds only Tb = T diag(beta), M and G
+// (33 KB instead of the 148 KB W/U/Q/K^T/M record): the chunk update is
+// regrouped as
+//   D = U - W S = Tb (v_scale V - diag(e^G) k_scale K S).
+
+// Per (value head, chunk): A = beta_i e^{G_i-G_j} k_i.k_j (j < i) and
+// M = q_scale k_scale e^{G_i-G_j} q_i.k_j (j <= i) on exact bf16 MFMA,
+// T = (I + A)^-1, and the record (Tb split, M split, G).
+struct TbShared {
+  bf16_bits k[kChunk][kChunkDim + 8];
+  bf16_bits q[kChunk][kChunkDim + 8];
+  float a[kChunk][kLdC];
+  float tm[kChunk][kLdC];
+  float mm[kChunk][kLdC];
+  float y[32][36];
+  float g[kChunk];
+  float beta[kChunk];
+};
+
+// Writes a [64][64] fp32 LDS tile (times the per-column factor col[j], or 1)
+// to a record as split bf16 [2][64][64]: thread -> row tid / 4, columns
+// 16 (tid % 4) .. +15.
+__device__ __forceinline__ void write_split_64(const float (*src)[kLdC], const float *col, bf16_bits *dst) {
+  const int i = threadIdx.x >> 2, j0 = 16 * (threadIdx.x & 3);
+  u32x4 hi[2], lo[2];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int j = j0 + 2 * e;
+    std::uint32_t hw, lw;
+    split2(src[i][j] * (col ? col[j] : 1.f), src[i][j + 1] * (col ? col[j + 1] : 1.f), hw, lw);
+    hi[e >> 2][e & 3] = hw;
+    lo[e >> 2][e & 3] = lw;
+  }
+  bf16_bits *row = dst + i * kChunk + j0;
+  reinterpret_cast<u32x4 *>(row)[0] = hi[0];
+  reinterpret_cast<u32x4 *>(row)[1] = hi[1];
+  reinterpret_cast<u32x4 *>(row + kChunk * kChunk)[0] = lo[0];
+  reinterpret_cast<u32x4 *>(row + kChunk * kChunk)[1] = lo[1];
+}
+
+__global__ __launch_bounds__(256) void chunk_tb_kernel(Src<bf16_bits> qs, Src<bf16_bits> ks,
+                                                       const float *__restrict__ beta,
+                                                       const float *__restrict__ gdecay,
+                                                       ChunkScratch scratch, std::size_t tokens,
+                                                       std::size_t hk, std::size_t hv) {
+  __shared__ TbShared sh;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 15, lk = lane >> 4;
+  const std::size_t h = blockIdx.x;
+  const std::size_t kh = h % hk;
+  const std::size_t t0 = static_cast<std::size_t>(blockIdx.y) * kChunk;
+  const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
+  unsigned char *record = scratch.at(h, blockIdx.y);
+
+  // K and Q rows: item tid + 256 r -> row item / 16, dims 8 (item % 16) ..
+  // +7; rows past L repeat row L-1.
+  u32x4 kv[4], qv[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int p = tid + 256 * r, i = p >> 4, d = 8 * (p & 15);
+    const std::size_t t = t0 + (i < L ? i : L - 1);
+    kv[r] = *reinterpret_cast<const u32x4 *>(src_row(ks, t, kh, d));
+    qv[r] = *reinterpret_cast<const u32x4 *>(src_row(qs, t, kh, d));
+  }
+  float bt = 0.f, gt = 0.f;
+  if (tid < L) {
+    bt = beta[(t0 + tid) * hv + h];
+    gt = gdecay[(t0 + tid) * hv + h];
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int p = tid + 256 * r, i = p >> 4, d = 8 * (p & 15);
+    *reinterpret_cast<u32x4 *>(&sh.k[i][d]) = kv[r];
+    *reinterpret_cast<u32x4 *>(&sh.q[i][d]) = qv[r];
+  }
+  if (tid < kChunk) {
+    sh.beta[tid] = bt;
+    sh.g[tid] = gt;
+  }
+  __syncthreads();
+  if (wave == 0) sh.g[lane] = wave_prefix_sum(sh.g[lane]); // rows past L repeat G[L-1] (g = 0)
+  __syncthreads();
+  // A and M: wave w takes row tile w and column tiles 0 .. w (tiles right of
+  // the diagonal are 0).
+  {
+    const float kk_scale = ks.scale * ks.scale, qk_scale = qs.scale * ks.scale;
+    float gi[4], bi[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      gi[r] = sh.g[16 * wave + 4 * lk + r];
+      bi[r] = sh.beta[16 * wave + 4 * lk + r] * kk_scale;
+    }
+    bf16x8 krow[4], qrow[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      krow[n] = lds8(&sh.k[16 * wave + lr][32 * n + 8 * lk]);
+      qrow[n] = lds8(&sh.q[16 * wave + lr][32 * n + 8 * lk]);
+    }
+    for (int tj = 0; tj < 4; ++tj) {
+      const int j = 16 * tj + lr;
+      if (tj > wave) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sh.mm[16 * wave + 4 * lk + r][j] = 0.f;
+        continue;
+      }
+      bf16x8 kcol[4];
+#pragma unroll
+      for (int n = 0; n < 4; ++n) kcol[n] = lds8(&sh.k[16 * tj + lr][32 * n + 8 * lk]);
+      floatx4 aa = floatx4{}, am = floatx4{};
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        aa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(krow[n], kcol[n], aa, 0, 0, 0);
+        am = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qrow[n], kcol[n], am, 0, 0, 0);
+      }
+      const float gj = sh.g[j];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * wave + 4 * lk + r;
+        const float e = __expf(gi[r] - gj);
+        sh.a[i][j] = (j < i && i < L) ? bi[r] * e * aa[r] : 0.f;
+        sh.mm[i][j] = (j <= i && i < L) ? qk_scale * e * am[r] : 0.f;
+      }
+    }
+  }
+  __syncthreads();
+  invert_unit_lower_64(sh.a, sh.tm, sh.y);
+  write_split_64(sh.tm, sh.beta, reinterpret_cast<bf16_bits *>(record + rec2::kTb));
+  write_split_64(sh.mm, nullptr, reinterpret_cast<bf16_bits *>(record + rec2::kM));
+  if (tid < kChunk) reinterpret_cast<float *>(record + rec2::kG)[tid] = sh.g[tid];
+}
+
+// Operands of one chunk, staged in LDS by LDS-direct loads.  Q and K rows use
+// the 128-wide swizzle (16-byte chunk c of row r at c ^ (r & 15)), Tb and M
+// the 64-wide one (c ^ ((r >> 1) & 7)).
+struct TScanBuf {
+  bf16_bits q[kChunk][kChunkDim];
+  bf16_bits k[kChunk][kChunkDim];
+  bf16_bits tb[2][kChunk][kChunk];
+  bf16_bits m[2][kChunk][kChunk];
+  bf16_bits v[kChunk][kColBlock]; // V[i][c0 ..]
+  float g[kChunk];
+};
+
+struct TScanShared {
+  TScanBuf buf[2];                  // chunk c in buf[c & 1]
+  bf16_bits st[2][kColBlock][kLdK]; // S^T (hi, lo), [c][d]
+  bf16_bits yt[2][kColBlock][kLdJ]; // (v_scale V - e^G k_scale K S)^T (hi, lo), [c][j]
+  bf16_bits dt[2][kColBlock][kLdJ]; // D^T (hi, lo)
+  bf16_bits ft[2][kColBlock][kLdJ]; // (e^{G_last-G} D)^T (hi, lo)
+  float qo[kChunk][kColBlock];      // e^G q_scale Q S, from waves 0-3 to waves 4-7
+};
+
+constexpr int kTScanThreads = 512;
+
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4v;
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i % 4
+// of the 8 bytes that lanes 4 e + i / 4 (e = 0..3) address.
+__device__ __forceinline__ u32x2 lds_tr16_b64(const bf16_bits *p) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v *)(p)));
+}
+
+// Issues the LDS-direct loads of chunk t0 (L tokens) into `b` from loader
+// wave u = 0..3: Q and K rows 16u .. 16u+15, half u / 2 of Tb and M (rows
+// 32 (u % 2) .. +31); loaders 0 and 1 load V rows 32u .. +31 (this block's 16
+// columns), loader 2 loads G.  Rows past L repeat row L-1.
+__device__ __forceinline__ void tscan_issue(TScanBuf &b, const Src<bf16_bits> &qs, const Src<bf16_bits> &ks,
+                                            const Src<bf16_bits> &vs, const unsigned char *record,
+                                            std::size_t t0, int L, std::size_t h, std::size_t kh, int c0,
+                                            int u) {
+  const int lane = threadIdx.x & 63;
+  const bf16_bits *qb = qs.base + t0 * qs.row + kh * qs.head_stride;
+  const bf16_bits *kb = ks.base + t0 * ks.row + kh * ks.head_stride;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row0 = 16 * u + 4 * j, row = row0 + (lane >> 4), p = lane & 15;
+    const int src = row < L ? row : L - 1;
+    const std::uint32_t chunk = static_cast<std::uint32_t>((p ^ (row & 15)) * 16);
+    load_lds_b128(qb, static_cast<std::uint32_t>(src * qs.row * 2) + chunk, lds_address(&b.q[row0][0]));
+    load_lds_b128(kb, static_cast<std::uint32_t>(src * ks.row * 2) + chunk, lds_address(&b.k[row0][0]));
+  }
+  const int half = u >> 1, rows = 32 * (u & 1);
+  load_rows_lds<kChunk, kChunk, 32, 1>(record, static_cast<std::uint32_t>(rec2::kTb + half * kChunk * kChunk * 2),
+                                       &b.tb[half], rows);
+  load_rows_lds<kChunk, kChunk, 32, 1>(record, static_cast<std::uint32_t>(rec2::kM + half * kChunk * kChunk * 2),
+                                       &b.m[half], rows);
+  if (u < 2) {
+    const int row = 32 * u + (lane >> 1), src = row < L ? row : L - 1;
+    const bf16_bits *vb = vs.base + t0 * vs.row + h * vs.head_stride + c0;
+    load_lds_b128(vb, static_cast<std::uint32_t>(src * vs.row * 2 + (lane & 1) * 16),
+                  lds_address(&b.v[32 * u][0]));
+  } else if (u == 2 && lane < 16) {
+    load_lds_b128(record, static_cast<std::uint32_t>(rec2::kG + 16 * lane), lds_address(&b.g[0]));
+  }
+}
+
+// Block (value head, 16-column block), sequential over chunks, 8 waves.  Per
+// chunk, with row tiles rt = 0..3 of the chunk and S^T / D^T in LDS:
+//   1. waves 0-3: X = K S and QS for rows rt = w (one read of S^T for both),
+//      Y = v_scale V - e^G k_scale X -> yt;
+//   2. waves 0-3: D = Tb Y (rows w) -> dt, e^{G_last-G} D -> ft;
+//   3. waves 0-3: S' = e^{G_last} S + k_scale K^T ft for state rows 32w ..
+//      +31 (fp32 in VGPRs, then S'^T -> st); waves 4-7: O = e^G q_scale QS +
+//      M D for rows w-4 (QS handed over through LDS in step 1).
+// Waves 4-7, idle in steps 1 and 2, issue the loads of the next chunk's
+// operands into the other buffer, so waves 0-3 never wait on memory.
+template <typename OutT>
+__global__ __launch_bounds__(kTScanThreads) void chunk_tscan_kernel(Src<bf16_bits> qs, Src<bf16_bits> ks,
+                                                                    Src<bf16_bits> vs, ChunkScratch scratch,
+                                                                    float *__restrict__ state,
+                                                                    OutT *__restrict__ out,
+                                                                    std::size_t tokens, std::size_t hk,
+                                                                    std::size_t hv) {
+  __shared__ TScanShared sh;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lk = lane >> 4;
+  const std::size_t h = blockIdx.x;
+  const std::size_t kh = h % hk;
+  const int c0 = blockIdx.y * kColBlock;
+  const float q_scale = qs.scale, k_scale = ks.scale, v_scale = vs.scale;
+  float *sg = state + h * kChunkDim * kChunkDim;
+  if (wave >= 4)
+    tscan_issue(sh.buf[0], qs, ks, vs, scratch.at(h, 0), 0, static_cast<int>(tokens < kChunk ? tokens : kChunk),
+                h, kh, c0, wave - 4);
+  // fp32 state: waves 0-3 hold s[tt] = S[32 w + 16 tt + 4 lk + r][c0 + lr].
+  floatx4 s[2];
+  if (wave < 4) {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[tt][r] = sg[(32 * wave + 16 * tt + 4 * lk + r) * kChunkDim + c0 + lr];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) store_split_t<kLdK>(sh.st[0], sh.st[1], 32 * wave + 16 * tt, s[tt]);
+  }
+  // Waves 4-7 store a chunk's output rows at the start of the next chunk, so
+  // the wait for that chunk's loads does not also wait for fresh stores.
+  floatx4 pend_o = floatx4{};
+  std::size_t pend_t0 = 0;
+  int pend_l = 0;
+  auto store_o = [&](std::size_t ot0, int ol) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * (wave & 3) + 4 * lk + r;
+      if (i < ol) Elem<OutT>::store(out, ((ot0 + i) * hv + h) * kChunkDim + c0 + lr, pend_o[r]);
+    }
+  };
+  const int rt = wave & 3, i0 = 16 * rt;
+  for (std::size_t c = 0, t0 = 0; t0 < tokens; ++c, t0 += kChunk) {
+    const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
+    const TScanBuf &b = sh.buf[c & 1];
+    if (wave >= 4) wait_vm<0>(); // loads of chunk c (and the stores of chunk c - 2)
+    __syncthreads();             // every loader's loads, S^T, and the last chunk's reads done
+    if (wave >= 4) {
+      store_o(pend_t0, pend_l); // chunk c - 1 (none before chunk 1: pend_l = 0)
+      if (t0 + kChunk < tokens) {
+        const std::size_t t1 = t0 + kChunk;
+        tscan_issue(sh.buf[(c + 1) & 1], qs, ks, vs, scratch.at(h, c + 1), t1,
+                    static_cast<int>(tokens - t1 < kChunk ? tokens - t1 : kChunk), h, kh, c0, wave - 4);
+      }
+    }
+    const float glast = b.g[kChunk - 1]; // = G[L-1] (padded)
+    // ---- 1
+    if (wave < 4) {
+      floatx4 x0 = floatx4{}, x1 = floatx4{}, q0 = floatx4{}, q1 = floatx4{};
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const int ro = swz128(i0 + lr, 4 * n + lk);
+        const bf16x8 ka = lds8(&b.k[0][0] + ro), qa = lds8(&b.q[0][0] + ro);
+        const bf16x8 sth = lds8(&sh.st[0][lr][32 * n + 8 * lk]), stl = lds8(&sh.st[1][lr][32 * n + 8 * lk]);
+        x0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, sth, x0, 0, 0, 0);
+        x1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, stl, x1, 0, 0, 0);
+        q0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa, sth, q0, 0, 0, 0);
+        q1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa, stl, q1, 0, 0, 0);
+      }
+      floatx4 y, o;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = i0 + 4 * lk + r;
+        const float eg = __expf(b.g[i]);
+        y[r] = v_scale * bf16_lo(b.v[i][lr]) - eg * k_scale * (x0[r] + x1[r]);
+        o[r] = eg * q_scale * (q0[r] + q1[r]);
+      }
+      store_split_t<kLdJ>(sh.yt[0], sh.yt[1], i0, y);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sh.qo[i0 + 4 * lk + r][lr] = o[r];
+    }
+    __syncthreads();
+    // ---- 2
+    if (wave < 4) {
+      floatx4 d0 = floatx4{}, d1 = floatx4{}, d2 = floatx4{};
+      const int steps = rt < 2 ? 1 : 2; // Tb is lower triangular
+      for (int n = 0; n < steps; ++n) {
+        const int to = swz64(i0 + lr, 4 * n + lk);
+        const bf16x8 th = lds8(&b.tb[0][0][0] + to), tl = lds8(&b.tb[1][0][0] + to);
+        const bf16x8 yh = lds8(&sh.yt[0][lr][32 * n + 8 * lk]), yl = lds8(&sh.yt[1][lr][32 * n + 8 * lk]);
+        d0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(th, yh, d0, 0, 0, 0);
+        d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(th, yl, d1, 0, 0, 0);
+        d2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tl, yh, d2, 0, 0, 0);
+      }
+      floatx4 dv, fv;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = i0 + 4 * lk + r;
+        dv[r] = d0[r] + (d1[r] + d2[r]);
+        fv[r] = i < L ? __expf(glast - b.g[i]) * dv[r] : 0.f;
+      }
+      store_split_t<kLdJ>(sh.dt[0], sh.dt[1], i0, dv);
+      store_split_t<kLdJ>(sh.ft[0], sh.ft[1], i0, fv);
+    }
+    __syncthreads();
+    // ---- 3
+    if (wave < 4) {
+      const float egl = __expf(glast);
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int d0 = 32 * wave + 16 * tt;
+        // K^T operand (rows d0 + lr, keys 32 n + 8 lk .. +7) by transposed
+        // reads of the K rows: source lane r of a 16-lane group supplies dims
+        // d0 + 4 (r & 3) .. +3 of key (r >> 2) of a 4-key block.
+        const int dsrc = d0 + 4 * (lr & 3);
+        floatx4 a0 = floatx4{}, a1 = floatx4{};
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+          u32x2 part[2];
+#pragma unroll
+          for (int hq = 0; hq < 2; ++hq) {
+            const int j = 32 * n + 8 * lk + 4 * hq + (lr >> 2);
+            part[hq] = lds_tr16_b64(&b.k[0][0] + swz128(j, dsrc >> 3) + (dsrc & 7));
+          }
+          const bf16x8 kt = __builtin_bit_cast(bf16x8, u32x4{part[0][0], part[0][1], part[1][0], part[1][1]});
+          const bf16x8 fh = lds8(&sh.ft[0][lr][32 * n + 8 * lk]), fl = lds8(&sh.ft[1][lr][32 * n + 8 * lk]);
+          a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt, fh, a0, 0, 0, 0);
+          a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt, fl, a1, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s[tt][r] = fmaf(egl, s[tt][r], k_scale * (a0[r] + a1[r]));
+        store_split_t<kLdK>(sh.st[0], sh.st[1], d0, s[tt]);
+      }
+    } else {
+      floatx4 m0 = floatx4{}, m1 = floatx4{}, m2 = floatx4{};
+      const int steps = rt < 2 ? 1 : 2; // M is lower triangular
+      for (int n = 0; n < steps; ++n) {
+        const int mo = swz64(i0 + lr, 4 * n + lk);
+        const bf16x8 mh = lds8(&b.m[0][0][0] + mo), ml = lds8(&b.m[1][0][0] + mo);
+        const bf16x8 dh = lds8(&sh.dt[0][lr][32 * n + 8 * lk]), dl = lds8(&sh.dt[1][lr][32 * n + 8 * lk]);
+        m0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mh, dh, m0, 0, 0, 0);
+        m1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mh, dl, m1, 0, 0, 0);
+        m2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ml, dh, m2, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pend_o[r] = sh.qo[i0 + 4 * lk + r][lr] + (m0[r] + (m1[r] + m2[r]));
+      pend_t0 = t0;
+      pend_l = L;
+    }
+  }
+  if (wave >= 4) store_o(pend_t0, pend_l);
+  if (wave < 4) {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sg[(32 * wave + 16 * tt + 4 * lk + r) * kChunkDim + c0 + lr] = s[tt][r];
+  }
 }
 
 // ----------------------------------------------------- stage 3 kernel
@@ -1740,16 +1860,17 @@ void launch_recurrence(Src<InT> q, Src<InT> k, Src<InT> v, const float *beta, co
                        hipStream_t stream) {
   if (chunked) {
     const dim3 pgrid{static_cast<unsigned>(hv), static_cast<unsigned>(ceil_div_unchecked(tokens, kChunk)), 1};
-    if constexpr (std::is_same_v<InT, bf16_bits>)
-      chunk_prep_bf16_kernel<<<pgrid, kPrepThreads, 0, stream>>>(q, k, v, beta, g, scratch, tokens, hk, hv);
-    else
-      chunk_prep_kernel<InT><<<pgrid, 256, 0, stream>>>(q, k, v, beta, g, scratch, tokens, hk, hv);
-    check_launch<Err>("qwen35_gated_delta chunk preparation");
     const dim3 sgrid{static_cast<unsigned>(hv), kChunkDim / kColBlock, 1};
-    constexpr bool exact = std::is_same_v<InT, bf16_bits>;
-    chunk_scan_kernel<exact, OutT><<<sgrid, 256, 0, stream>>>(scratch, state, out, tokens, hv,
-                                                              exact ? q.scale : 1.0f,
-                                                              exact ? k.scale : 1.0f);
+    if constexpr (std::is_same_v<InT, bf16_bits>) {
+      chunk_tb_kernel<<<pgrid, 256, 0, stream>>>(q, k, beta, g, scratch, tokens, hk, hv);
+      check_launch<Err>("qwen35_gated_delta chunk preparation");
+      chunk_tscan_kernel<OutT><<<sgrid, kTScanThreads, 0, stream>>>(q, k, v, scratch, state, out, tokens, hk, hv);
+      check_launch<Err>("qwen35_gated_delta chunk scan");
+      return;
+    }
+    chunk_prep_kernel<InT><<<pgrid, 256, 0, stream>>>(q, k, v, beta, g, scratch, tokens, hk, hv);
+    check_launch<Err>("qwen35_gated_delta chunk preparation");
+    chunk_scan_kernel<OutT><<<sgrid, 256, 0, stream>>>(scratch, state, out, tokens, hv);
     check_launch<Err>("qwen35_gated_delta chunk scan");
     return;
   }
@@ -1806,6 +1927,7 @@ void launch_typed(const DeltaSources &src, const void *conv_weight, const void *
     scratch.rec = reinterpret_cast<unsigned char *>(ws) +
                   record_offset(s.tokens * (c.conv_dim + s.hidden_size + 2 * s.value_heads) * sizeof(float));
     scratch.chunks = ceil_div_unchecked(s.tokens, kChunk);
+    scratch.bytes = rec::kBytes;
   }
 
   const bool fast = s.key_dim == kChunkDim && s.value_dim == kChunkDim && s.conv_width == 4 &&
@@ -2061,7 +2183,7 @@ void qwen35_gated_delta_unpacked(const void *qkv, const void *beta, const void *
 std::size_t qwen35_gated_delta_core_workspace_bytes(GatedDeltaCoreShape s) {
   require<Err>(s.tokens > 0 && s.key_heads > 0 && s.value_heads > 0 && s.key_dim > 0 && s.value_dim > 0,
                "gated-delta core shape must be positive");
-  return chunk_record_bytes(s.tokens, s.value_heads, s.key_dim, s.value_dim);
+  return chunk_record_bytes(s.tokens, s.value_heads, s.key_dim, s.value_dim, rec2::kBytes);
 }
 
 void qwen35_gated_delta_core(const void *q, const void *k, const void *v, const float *beta,
@@ -2090,6 +2212,7 @@ void qwen35_gated_delta_core(const void *q, const void *k, const void *v, const 
   if (chunked) {
     scratch.rec = static_cast<unsigned char *>(workspace);
     scratch.chunks = ceil_div_unchecked(s.tokens, kChunk);
+    scratch.bytes = rec2::kBytes;
   }
   launch_recurrence<bf16_bits, bf16_bits>(qs, ks, vs, beta, log_decay, state,
                                           static_cast<bf16_bits *>(output), scratch, s.tokens,

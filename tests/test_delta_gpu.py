@@ -197,6 +197,18 @@ def test_cfg5_chunked_prefill_then_32_decode_steps(gpu):
     assert rel_l2(s, ws_) < 1e-4
 
 
+@pytest.mark.parametrize("T", [1, 63, 64, 65, 130, 257])
+def test_core_chunked_ragged_lengths_with_state(gpu, T):
+    """Chunked core on a last chunk of every fill (1, 63, 64, 65 tokens ...)
+    from a non-zero state, against the oracle's token recurrence."""
+    q, k, v, beta, g = cfg5_inputs(T, 100 + T)
+    s0 = normal(rng(200 + T), 32, 128, 128, scale=0.05)
+    want_o, want_s = orc.delta_core(q, k, v, beta, g, 1 / np.sqrt(128), s0)
+    got_o, got_s = run_core(q, k, v, beta, g, s0, chunked=True)
+    assert rel_l2(got_s, want_s) < 1e-4
+    assert_bf16_close(got_o, bf16(want_o), what=f"chunked core T={T}")
+
+
 def test_core_chunked_equals_recurrent(gpu):
     T = 200
     q, k, v, beta, g = cfg5_inputs(T, 7)
