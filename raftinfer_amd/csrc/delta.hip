@@ -1866,12 +1866,12 @@ void launch_recurrence(Src<InT> q, Src<InT> k, Src<InT> v, const float *beta, co
       check_launch<Err>("qwen35_gated_delta chunk preparation");
       chunk_tscan_kernel<OutT><<<sgrid, kTScanThreads, 0, stream>>>(q, k, v, scratch, state, out, tokens, hk, hv);
       check_launch<Err>("qwen35_gated_delta chunk scan");
-      return;
+    } else {
+      chunk_prep_kernel<InT><<<pgrid, 256, 0, stream>>>(q, k, v, beta, g, scratch, tokens, hk, hv);
+      check_launch<Err>("qwen35_gated_delta chunk preparation");
+      chunk_scan_kernel<OutT><<<sgrid, 256, 0, stream>>>(scratch, state, out, tokens, hv);
+      check_launch<Err>("qwen35_gated_delta chunk scan");
     }
-    chunk_prep_kernel<InT><<<pgrid, 256, 0, stream>>>(q, k, v, beta, g, scratch, tokens, hk, hv);
-    check_launch<Err>("qwen35_gated_delta chunk preparation");
-    chunk_scan_kernel<OutT><<<sgrid, 256, 0, stream>>>(scratch, state, out, tokens, hv);
-    check_launch<Err>("qwen35_gated_delta chunk scan");
     return;
   }
   if (dk == 128 && dv == 128 && (reinterpret_cast<std::uintptr_t>(state) & 15u) == 0) {
