@@ -1079,7 +1079,18 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
   __syncthreads();
 
   // M = e^{G_i-G_j} (q_i . k_j), j <= i, and A = beta_i e^{G_i-G_j} (k_i . k_j),
-  // j < i, on fp32 MFMA 16x16x4; wave w = row tile w.
+  // j < i, on fp32 MFMA 16x16x4; wave w = row tile w.  The per-row G and
+  // beta are read once, before the products, and every entry is formed
+  // unconditionally and masked by a multiply (a select would put its LDS
+  // reads behind a branch each).
+  float gi[4], bi[4], mi[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int i = wave * 16 + lk * 4 + r;
+    gi[r] = sh.g[i];
+    bi[r] = sh.beta[i];
+    mi[r] = i < L ? 1.f : 0.f;
+  }
   for (int tj = 0; tj < 4; ++tj) {
     floatx4 am = floatx4{}, aa = floatx4{};
     if (tj <= wave) {
@@ -1090,12 +1101,16 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(Src<InT> qs, Src<InT> k
         aa = mfma4(sh.k[wave * 16 + lr][k0 + lk], kj, aa);
       }
     }
+    const int j = tj * 16 + lr;
+    const float gj = sh.g[j];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int i = wave * 16 + lk * 4 + r, j = tj * 16 + lr;
-      const float e = __expf(sh.g[i] - sh.g[j]);
-      sh.mm[i][j] = (j <= i && i < L) ? am[r] * e : 0.f;
-      sh.a[i][j] = (j < i && i < L) ? sh.beta[i] * e * aa[r] : 0.f;
+      const int i = wave * 16 + lk * 4 + r;
+      // Only j <= i is kept; clamping keeps e^{G_i-G_j} finite above the
+      // diagonal (G_i > G_j there) so the masking multiply gives 0, not NaN.
+      const float e = __expf(fminf(gi[r] - gj, 0.f)) * mi[r];
+      sh.mm[i][j] = (j <= i ? 1.f : 0.f) * (am[r] * e);
+      sh.a[i][j] = (j < i ? 1.f : 0.f) * (bi[r] * e * aa[r]);
     }
   }
   // Q and K^T go to the record before Q's LDS is reused, as
@@ -1479,17 +1494,36 @@ struct TbShared {
   float beta[kChunk];
 };
 
-// Writes a [64][64] fp32 LDS tile (times the per-column factor col[j], or 1)
-// to a record as split bf16 [2][64][64]: thread -> row tid / 4, columns
-// 16 (tid % 4) .. +15.
+// Writes a [64][64] fp32 LDS tile (times the per-column factor col[j] when
+// kCol) to a record as split bf16 [2][64][64]: thread -> row tid / 4,
+// columns 16 (tid % 4) .. +15.  All LDS reads go out before the first use.
+template <bool kCol>
 __device__ __forceinline__ void write_split_64(const float (*src)[kLdC], const float *col, bf16_bits *dst) {
   const int i = threadIdx.x >> 2, j0 = 16 * (threadIdx.x & 3);
+  float v[16];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float4 x = *reinterpret_cast<const float4 *>(&src[i][j0 + 4 * e]);
+    v[4 * e] = x.x;
+    v[4 * e + 1] = x.y;
+    v[4 * e + 2] = x.z;
+    v[4 * e + 3] = x.w;
+  }
+  if constexpr (kCol) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float4 c = *reinterpret_cast<const float4 *>(&col[j0 + 4 * e]);
+      v[4 * e] *= c.x;
+      v[4 * e + 1] *= c.y;
+      v[4 * e + 2] *= c.z;
+      v[4 * e + 3] *= c.w;
+    }
+  }
   u32x4 hi[2], lo[2];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const int j = j0 + 2 * e;
     std::uint32_t hw, lw;
-    split2(src[i][j] * (col ? col[j] : 1.f), src[i][j + 1] * (col ? col[j + 1] : 1.f), hw, lw);
+    split2(v[2 * e], v[2 * e + 1], hw, lw);
     hi[e >> 2][e & 3] = hw;
     lo[e >> 2][e & 3] = lw;
   }
@@ -1586,8 +1620,8 @@ __global__ __launch_bounds__(256) void chunk_tb_kernel(Src<bf16_bits> qs, Src<bf
   }
   __syncthreads();
   invert_unit_lower_64(sh.a, sh.tm, sh.y);
-  write_split_64(sh.tm, sh.beta, reinterpret_cast<bf16_bits *>(record + rec2::kTb));
-  write_split_64(sh.mm, nullptr, reinterpret_cast<bf16_bits *>(record + rec2::kM));
+  write_split_64<true>(sh.tm, sh.beta, reinterpret_cast<bf16_bits *>(record + rec2::kTb));
+  write_split_64<false>(sh.mm, nullptr, reinterpret_cast<bf16_bits *>(record + rec2::kM));
   if (tid < kChunk) reinterpret_cast<float *>(record + rec2::kG)[tid] = sh.g[tid];
 }
 
@@ -1750,6 +1784,9 @@ __global__ __launch_bounds__(kTScanThreads) void chunk_tscan_kernel(Src<bf16_bit
     __syncthreads();
     // ---- 2
     if (wave < 4) {
+      floatx4 fdec;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) fdec[r] = __expf(glast - b.g[i0 + 4 * lk + r]);
       floatx4 d0 = floatx4{}, d1 = floatx4{}, d2 = floatx4{};
       const int steps = rt < 2 ? 1 : 2; // Tb is lower triangular
       for (int n = 0; n < steps; ++n) {
@@ -1760,12 +1797,15 @@ __global__ __launch_bounds__(kTScanThreads) void chunk_tscan_kernel(Src<bf16_bit
         d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(th, yl, d1, 0, 0, 0);
         d2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tl, yh, d2, 0, 0, 0);
       }
+      // The decay factors are formed unconditionally (G is padded past L, so
+      // they are finite there) and masked by a multiply: a select on i < L
+      // would put each G read behind its own branch and LDS round trip.
       floatx4 dv, fv;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = i0 + 4 * lk + r;
         dv[r] = d0[r] + (d1[r] + d2[r]);
-        fv[r] = i < L ? __expf(glast - b.g[i]) * dv[r] : 0.f;
+        fv[r] = (i < L ? 1.f : 0.f) * (fdec[r] * dv[r]);
       }
       store_split_t<kLdJ>(sh.dt[0], sh.dt[1], i0, dv);
       store_split_t<kLdJ>(sh.ft[0], sh.ft[1], i0, fv);
