@@ -32,6 +32,7 @@
 #include "raftinfer_amd/qwen35_delta.hpp"
 
 #include <cmath>
+#include <type_traits>
 
 namespace raftinfer::kernels {
 namespace {
@@ -904,92 +905,116 @@ __device__ __forceinline__ const T *src_row(const Src<T> &s, std::size_t t, std:
 //      substitution, lane = column (all four blocks at once);
 //   2. waves 0 and 1 form the two 16 x 16 off-diagonal blocks of the 32 x 32
 //      diagonal blocks;
-//   3. all four waves form the 32 x 32 lower-left block, one 16 x 16 tile each.
-// Products run on fp32 MFMA 16x16x4; `y` is 32 x 36 fp32 scratch.  Ends with a
-// barrier; T's strictly upper part is written as 0.
+//   3. waves 0-3 form the 32 x 32 lower-left block, one 16 x 16 tile each, in
+//      two products (3a, 3b).
+// Products run on fp32 MFMA 16x16x4; `y` is 32 x 36 fp32 scratch.  Each step
+// reads what the previous ones wrote, so a barrier separates them.  T's
+// strictly upper part is written as 0.
+
+// Step 1 for diagonal block w, by wave w: zeros rows 16w .. 16w+15 right of
+// the block, then lanes 0..15 (lane = column) substitute.  entry(r, j) gives
+// A[16w + r][16w + j] for j < r (the same value in every lane).
+template <typename Entry>
+__device__ __forceinline__ void invert_step1(float (*tm)[kLdC], int w, Entry entry) {
+  const int lane = threadIdx.x & 63;
+  const int b = 16 * w;
+  for (int j = 16 * (w + 1) + lane; j < kChunk; j += 64)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) tm[b + r][j] = 0.f;
+  float x[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) x[r] = r == lane ? 1.f : 0.f;
+  // Right-looking: once x[j] is final, the updates of rows j+1.. are
+  // independent, so the dependent chain is 15 FMAs long, not 120.
+#pragma unroll
+  for (int j = 0; j < 15; ++j)
+#pragma unroll
+    for (int r = j + 1; r < 16; ++r) x[r] = fmaf(-entry(r, j), x[j], x[r]);
+  if (lane < 16) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) tm[b + r][b + lane] = x[r];
+  }
+}
+
+// Step 2, block (2p+1, 2p) = -T_qq A_qp T_pp for p = w (waves 0, 1).
+__device__ __forceinline__ void invert_step2(const float (*a)[kLdC], float (*tm)[kLdC], float (*y)[36],
+                                             int w) {
+  const int lane = threadIdx.x & 63, lr = lane & 15, lk = lane >> 4;
+  const int P = 32 * w, Q = P + 16;
+  floatx4 acc = floatx4{};
+#pragma unroll
+  for (int k0 = 0; k0 < 16; k0 += 4) acc = mfma4(a[Q + lr][P + k0 + lk], tm[P + k0 + lk][P + lr], acc);
+  float(*yw)[36] = y + 16 * w;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) yw[4 * lk + r][lr] = acc[r];
+  wave_lds_order();
+  acc = floatx4{};
+#pragma unroll
+  for (int k0 = 0; k0 < 16; k0 += 4) acc = mfma4(tm[Q + lr][Q + k0 + lk], yw[k0 + lk][lr], acc);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) tm[Q + 4 * lk + r][P + lr] = -acc[r];
+}
+
+// Step 3a (waves 0-3): y tile (ti - 2, tj) = A_BL T_TL, ti = 2 + w / 2, tj = w % 2.
+__device__ __forceinline__ void invert_step3a(const float (*a)[kLdC], const float (*tm)[kLdC],
+                                              float (*y)[36], int w) {
+  const int lane = threadIdx.x & 63, lr = lane & 15, lk = lane >> 4;
+  const int ti = 2 + (w >> 1), tj = w & 1;
+  // T_TL is lower triangular and its upper right block is stored as 0, so the
+  // full k range gives the same sums; the operands are read up front.
+  float av[8], bv[8];
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    av[n] = a[16 * ti + lr][4 * n + lk];
+    bv[n] = tm[4 * n + lk][16 * tj + lr];
+  }
+  floatx4 acc = floatx4{};
+#pragma unroll
+  for (int n = 0; n < 8; ++n) acc = mfma4(av[n], bv[n], acc);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) y[16 * (ti - 2) + 4 * lk + r][16 * tj + lr] = acc[r];
+}
+
+// Step 3b (waves 0-3): T tile (ti, tj) = -T_BR y.
+__device__ __forceinline__ void invert_step3b(float (*tm)[kLdC], const float (*y)[36], int w) {
+  const int lane = threadIdx.x & 63, lr = lane & 15, lk = lane >> 4;
+  const int ti = 2 + (w >> 1), tj = w & 1;
+  // T_BR is lower triangular with its upper right block stored as 0.
+  float av[8], bv[8];
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    av[n] = tm[16 * ti + lr][32 + 4 * n + lk];
+    bv[n] = y[4 * n + lk][16 * tj + lr];
+  }
+  floatx4 acc = floatx4{};
+#pragma unroll
+  for (int n = 0; n < 8; ++n) acc = mfma4(av[n], bv[n], acc);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) tm[16 * ti + 4 * lk + r][16 * tj + lr] = -acc[r];
+}
+
+// Steps 2 and 3 with their barriers (every wave of the workgroup takes them;
+// waves 0-3 do the work), after step 1 and a barrier.  Ends with a barrier.
+__device__ __forceinline__ void invert_steps23(const float (*a)[kLdC], float (*tm)[kLdC], float (*y)[36]) {
+  const int wave = threadIdx.x >> 6;
+  if (wave < 2) invert_step2(a, tm, y, wave);
+  __syncthreads();
+  if (wave < 4) invert_step3a(a, tm, y, wave);
+  __syncthreads();
+  if (wave < 4) invert_step3b(tm, y, wave);
+  __syncthreads();
+}
+
+// All four steps, A read from LDS.  Ends with a barrier.
 __device__ __forceinline__ void invert_unit_lower_64(const float (*a)[kLdC], float (*tm)[kLdC],
                                                      float (*y)[36]) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int lr = lane & 15, lk = lane >> 4;
-  // Waves 0-3 do the work (a workgroup may have more); every wave takes the
-  // barriers.
-  // 1. Diagonal blocks; zero the blocks right of the diagonal.
+  const int wave = threadIdx.x >> 6;
   if (wave < 4) {
     const int b = 16 * wave;
-    for (int j = 16 * (wave + 1) + lane; j < kChunk; j += 64)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) tm[b + r][j] = 0.f;
-    if (lane < 16) {
-      float x[16], c[16][16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        x[r] = r == lane ? 1.f : 0.f;
-#pragma unroll
-        for (int j = 0; j < r; ++j) c[r][j] = a[b + r][b + j];
-      }
-      // Right-looking: once x[j] is final, the updates of rows j+1.. are
-      // independent, so the dependent chain is 15 FMAs long, not 120.
-#pragma unroll
-      for (int j = 0; j < 15; ++j)
-#pragma unroll
-        for (int r = j + 1; r < 16; ++r) x[r] = fmaf(-c[r][j], x[j], x[r]);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) tm[b + r][b + lane] = x[r];
-    }
+    invert_step1(tm, wave, [&](int r, int j) { return a[b + r][b + j]; });
   }
   __syncthreads();
-  // 2. Block (2p+1, 2p) = -T_qq A_qp T_pp for p = wave (waves 0, 1).
-  if (wave < 2) {
-    const int P = 32 * wave, Q = P + 16;
-    floatx4 acc = floatx4{};
-#pragma unroll
-    for (int k0 = 0; k0 < 16; k0 += 4)
-      acc = mfma4(a[Q + lr][P + k0 + lk], tm[P + k0 + lk][P + lr], acc);
-    float(*yw)[36] = y + 16 * wave;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) yw[4 * lk + r][lr] = acc[r];
-    wave_lds_order();
-    acc = floatx4{};
-#pragma unroll
-    for (int k0 = 0; k0 < 16; k0 += 4)
-      acc = mfma4(tm[Q + lr][Q + k0 + lk], yw[k0 + lk][lr], acc);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) tm[Q + 4 * lk + r][P + lr] = -acc[r];
-  }
-  __syncthreads();
-  // 3. Lower-left 32 x 32 block = -T_BR A_BL T_TL; wave w -> tile (2 + w/2, w%2).
-  const int ti = 2 + ((wave & 3) >> 1), tj = wave & 1;
-  if (wave < 4) {
-    // T_TL is lower triangular and its upper right block is stored as 0, so
-    // the full k range gives the same sums; the operands are read up front.
-    float av[8], bv[8];
-#pragma unroll
-    for (int n = 0; n < 8; ++n) {
-      av[n] = a[16 * ti + lr][4 * n + lk];
-      bv[n] = tm[4 * n + lk][16 * tj + lr];
-    }
-    floatx4 acc = floatx4{};
-#pragma unroll
-    for (int n = 0; n < 8; ++n) acc = mfma4(av[n], bv[n], acc);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) y[16 * (ti - 2) + 4 * lk + r][16 * tj + lr] = acc[r];
-  }
-  __syncthreads();
-  if (wave < 4) {
-    // T_BR is lower triangular with its upper right block stored as 0.
-    float av[8], bv[8];
-#pragma unroll
-    for (int n = 0; n < 8; ++n) {
-      av[n] = tm[16 * ti + lr][32 + 4 * n + lk];
-      bv[n] = y[4 * n + lk][16 * tj + lr];
-    }
-    floatx4 acc = floatx4{};
-#pragma unroll
-    for (int n = 0; n < 8; ++n) acc = mfma4(av[n], bv[n], acc);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) tm[16 * ti + 4 * lk + r][16 * tj + lr] = -acc[r];
-  }
-  __syncthreads();
+  invert_steps23(a, tm, y);
 }
 
 struct PrepShared {
@@ -1003,14 +1028,21 @@ struct PrepShared {
   float beta[kChunk];
 };
 
-// Inclusive prefix sum over the 64 lanes of a wave (Hillis-Steele).
+// Inclusive prefix sum over the 64 lanes of a wave: shifts within 16-lane
+// rows, then the row totals carried across rows, all on DPP (no LDS trip).
 __device__ __forceinline__ float wave_prefix_sum(float x) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const float y = __shfl_up(x, off);
-    if (lane >= off) x += y;
-  }
+  auto shr = [](float v, auto ctrl_tag) {
+    constexpr int kCtrl = decltype(ctrl_tag)::value;
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, false));
+  };
+  x += shr(x, std::integral_constant<int, 0x111>{}); // row_shr:1
+  x += shr(x, std::integral_constant<int, 0x112>{}); // row_shr:2
+  x += shr(x, std::integral_constant<int, 0x114>{}); // row_shr:4
+  x += shr(x, std::integral_constant<int, 0x118>{}); // row_shr:8
+  // row_bcast:15 adds lane 15 of row r to every lane of row r + 1 (rows 1, 3);
+  // row_bcast:31 adds lane 31 to every lane of rows 2 and 3.
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x142, 0xa, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x143, 0xc, 0xf, false));
   return x;
 }
 
@@ -1592,6 +1624,7 @@ __global__ __launch_bounds__(256) void chunk_tb_kernel(Src<bf16_bits> qs, Src<bf
       krow[n] = lds8(&sh.k[16 * wave + lr][32 * n + 8 * lk]);
       qrow[n] = lds8(&sh.q[16 * wave + lr][32 * n + 8 * lk]);
     }
+    floatx4 diag = floatx4{}; // this lane's part of A's diagonal tile (w, w)
     for (int tj = 0; tj < 4; ++tj) {
       const int j = 16 * tj + lr;
       if (tj > wave) {
@@ -1613,16 +1646,24 @@ __global__ __launch_bounds__(256) void chunk_tb_kernel(Src<bf16_bits> qs, Src<bf
       for (int r = 0; r < 4; ++r) {
         const int i = 16 * wave + 4 * lk + r;
         const float e = __expf(gi[r] - gj);
-        sh.a[i][j] = (j < i && i < L) ? bi[r] * e * aa[r] : 0.f;
+        const float av = (j < i && i < L) ? bi[r] * e * aa[r] : 0.f;
+        sh.a[i][j] = av;
+        if (tj == wave) diag[r] = av;
         sh.mm[i][j] = (j <= i && i < L) ? qk_scale * e * am[r] : 0.f;
       }
     }
+    // Step 1 of the inverse straight from the registers: A[16w + r][16w + j]
+    // is element r % 4 of lane 16 (r / 4) + j.
+    invert_step1(sh.tm, wave, [&](int r, int j) {
+      return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(diag[r & 3]), 16 * (r >> 2) + j));
+    });
   }
   __syncthreads();
-  invert_unit_lower_64(sh.a, sh.tm, sh.y);
-  write_split_64<true>(sh.tm, sh.beta, reinterpret_cast<bf16_bits *>(record + rec2::kTb));
+  // M and G are final here: their record stores drain during the inverse.
   write_split_64<false>(sh.mm, nullptr, reinterpret_cast<bf16_bits *>(record + rec2::kM));
   if (tid < kChunk) reinterpret_cast<float *>(record + rec2::kG)[tid] = sh.g[tid];
+  invert_steps23(sh.a, sh.tm, sh.y);
+  write_split_64<true>(sh.tm, sh.beta, reinterpret_cast<bf16_bits *>(record + rec2::kTb));
 }
 
 // Operands of one chunk, staged in LDS by LDS-direct loads.  Q and K rows use
