@@ -191,6 +191,11 @@ void validate_policy(const GatedDeltaLaunchPolicy &p, const GatedDeltaShape &s) 
 }
 
 // ---------------------------------------------------------- device math
+// Split of a float pair into packed (hi, lo) bf16 pairs.
+__device__ __forceinline__ void split2(float a, float b, std::uint32_t &h, std::uint32_t &l) {
+  h = pack_bf16x2(a, b);
+  l = pack_bf16x2(a - bf16_lo(h), b - bf16_hi(h));
+}
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
 __device__ __forceinline__ float sigmoid(float v) { return 1.0f / (1.0f + __expf(-v)); }
 __device__ __forceinline__ float softplus(float v) {
@@ -393,7 +398,11 @@ __global__ __launch_bounds__(256) void conv_norm_fast_kernel(
 // its shifted history, so no separate state update runs.  Same math as
 // conv_norm_kernel.
 constexpr int kConvWideChannels = 512;
-template <typename T, typename Wt, int W, int TT, bool kUpdateState>
+// kSplitOut: the convolved rows go out as two bf16 planes, x = hi + lo with
+// hi = bf16(x), lo = bf16(x - hi) (hi at element t * conv_dim + c of the
+// buffer, lo tokens * conv_dim elements further), the form the chunked scan
+// reads; otherwise as fp32 rows.
+template <typename T, typename Wt, int W, int TT, bool kUpdateState, bool kSplitOut = false>
 __global__ __launch_bounds__(64) void conv_norm_wide_kernel(
     DeltaRows<T> in, const Wt *__restrict__ conv_w, float *__restrict__ conv_state,
     const Wt *__restrict__ recurrent_a, const Wt *__restrict__ dt_bias, float *__restrict__ convolved,
@@ -458,9 +467,23 @@ __global__ __launch_bounds__(64) void conv_norm_wide_kernel(
 #pragma unroll
       for (int e = 0; e < 8; ++e) y[e] *= scale;
     }
-    float *dst = convolved + (t0 + u) * conv_dim + c;
-    *reinterpret_cast<float4 *>(dst) = make_float4(y[0], y[1], y[2], y[3]);
-    *reinterpret_cast<float4 *>(dst + 4) = make_float4(y[4], y[5], y[6], y[7]);
+    if constexpr (kSplitOut) {
+      u32x4 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        std::uint32_t hw, lw;
+        split2(y[2 * e], y[2 * e + 1], hw, lw);
+        hi[e] = hw;
+        lo[e] = lw;
+      }
+      bf16_bits *dst = reinterpret_cast<bf16_bits *>(convolved) + (t0 + u) * conv_dim + c;
+      *reinterpret_cast<u32x4 *>(dst) = hi;
+      *reinterpret_cast<u32x4 *>(dst + tokens * conv_dim) = lo;
+    } else {
+      float *dst = convolved + (t0 + u) * conv_dim + c;
+      *reinterpret_cast<float4 *>(dst) = make_float4(y[0], y[1], y[2], y[3]);
+      *reinterpret_cast<float4 *>(dst + 4) = make_float4(y[4], y[5], y[6], y[7]);
+    }
   }
   if constexpr (kUpdateState) {
     // one token: the new history of channel c + e is (slot 1, slot 2, cur)
@@ -1046,11 +1069,6 @@ __device__ __forceinline__ float wave_prefix_sum(float x) {
   return x;
 }
 
-// Split of a float pair into packed (hi, lo) bf16 pairs.
-__device__ __forceinline__ void split2(float a, float b, std::uint32_t &h, std::uint32_t &l) {
-  h = pack_bf16x2(a, b);
-  l = pack_bf16x2(a - bf16_lo(h), b - bf16_hi(h));
-}
 
 // Writes a [rows][cols] fp32 LDS tile (row stride LD) to a record as split
 // bf16 [2][rows][cols], 8 elements (two 16-byte stores) per item.
@@ -1515,9 +1533,11 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
 // Per (value head, chunk): A = beta_i e^{G_i-G_j} k_i.k_j (j < i) and
 // M = q_scale k_scale e^{G_i-G_j} q_i.k_j (j <= i) on exact bf16 MFMA,
 // T = (I + A)^-1, and the record (Tb split, M split, G).
-struct TbShared {
-  bf16_bits k[kChunk][kChunkDim + 8];
-  bf16_bits q[kChunk][kChunkDim + 8];
+// kSplit: q and k arrive as (hi, lo) bf16 planes (fp32 values split), and
+// each product is formed as hi*hi + hi*lo + lo*hi.
+template <bool kSplit> struct TbShared {
+  bf16_bits k[kSplit ? 2 : 1][kChunk][kChunkDim + 8];
+  bf16_bits q[kSplit ? 2 : 1][kChunk][kChunkDim + 8];
   float a[kChunk][kLdC];
   float tm[kChunk][kLdC];
   float mm[kChunk][kLdC];
@@ -1566,12 +1586,14 @@ __device__ __forceinline__ void write_split_64(const float (*src)[kLdC], const f
   reinterpret_cast<u32x4 *>(row + kChunk * kChunk)[1] = lo[1];
 }
 
-__global__ __launch_bounds__(256) void chunk_tb_kernel(Src<bf16_bits> qs, Src<bf16_bits> ks,
+template <bool kSplit>
+__global__ __launch_bounds__(256) void chunk_tb_kernel(Src<bf16_bits> qs, Src<bf16_bits> ks, std::size_t lo_plane,
                                                        const float *__restrict__ beta,
                                                        const float *__restrict__ gdecay,
                                                        ChunkScratch scratch, std::size_t tokens,
                                                        std::size_t hk, std::size_t hv) {
-  __shared__ TbShared sh;
+  constexpr int kHalves = kSplit ? 2 : 1;
+  __shared__ TbShared<kSplit> sh;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 15, lk = lane >> 4;
   const std::size_t h = blockIdx.x;
@@ -1580,27 +1602,31 @@ __global__ __launch_bounds__(256) void chunk_tb_kernel(Src<bf16_bits> qs, Src<bf
   const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
   unsigned char *record = scratch.at(h, blockIdx.y);
 
-  // K and Q rows: item tid + 256 r -> row item / 16, dims 8 (item % 16) ..
-  // +7; rows past L repeat row L-1.
-  u32x4 kv[4], qv[4];
+  // K and Q rows (each plane): item tid + 256 r -> row item / 16, dims
+  // 8 (item % 16) .. +7; rows past L repeat row L-1.
+  u32x4 kv[kHalves][4], qv[kHalves][4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int p = tid + 256 * r, i = p >> 4, d = 8 * (p & 15);
-    const std::size_t t = t0 + (i < L ? i : L - 1);
-    kv[r] = *reinterpret_cast<const u32x4 *>(src_row(ks, t, kh, d));
-    qv[r] = *reinterpret_cast<const u32x4 *>(src_row(qs, t, kh, d));
-  }
+  for (int hl = 0; hl < kHalves; ++hl)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int p = tid + 256 * r, i = p >> 4, d = 8 * (p & 15);
+      const std::size_t t = t0 + (i < L ? i : L - 1);
+      kv[hl][r] = *reinterpret_cast<const u32x4 *>(src_row(ks, t, kh, d) + hl * lo_plane);
+      qv[hl][r] = *reinterpret_cast<const u32x4 *>(src_row(qs, t, kh, d) + hl * lo_plane);
+    }
   float bt = 0.f, gt = 0.f;
   if (tid < L) {
     bt = beta[(t0 + tid) * hv + h];
     gt = gdecay[(t0 + tid) * hv + h];
   }
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int p = tid + 256 * r, i = p >> 4, d = 8 * (p & 15);
-    *reinterpret_cast<u32x4 *>(&sh.k[i][d]) = kv[r];
-    *reinterpret_cast<u32x4 *>(&sh.q[i][d]) = qv[r];
-  }
+  for (int hl = 0; hl < kHalves; ++hl)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int p = tid + 256 * r, i = p >> 4, d = 8 * (p & 15);
+      *reinterpret_cast<u32x4 *>(&sh.k[hl][i][d]) = kv[hl][r];
+      *reinterpret_cast<u32x4 *>(&sh.q[hl][i][d]) = qv[hl][r];
+    }
   if (tid < kChunk) {
     sh.beta[tid] = bt;
     sh.g[tid] = gt;
@@ -1618,12 +1644,14 @@ __global__ __launch_bounds__(256) void chunk_tb_kernel(Src<bf16_bits> qs, Src<bf
       gi[r] = sh.g[16 * wave + 4 * lk + r];
       bi[r] = sh.beta[16 * wave + 4 * lk + r] * kk_scale;
     }
-    bf16x8 krow[4], qrow[4];
+    bf16x8 krow[kHalves][4], qrow[kHalves][4];
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      krow[n] = lds8(&sh.k[16 * wave + lr][32 * n + 8 * lk]);
-      qrow[n] = lds8(&sh.q[16 * wave + lr][32 * n + 8 * lk]);
-    }
+    for (int hl = 0; hl < kHalves; ++hl)
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        krow[hl][n] = lds8(&sh.k[hl][16 * wave + lr][32 * n + 8 * lk]);
+        qrow[hl][n] = lds8(&sh.q[hl][16 * wave + lr][32 * n + 8 * lk]);
+      }
     floatx4 diag = floatx4{}; // this lane's part of A's diagonal tile (w, w)
     for (int tj = 0; tj < 4; ++tj) {
       const int j = 16 * tj + lr;
@@ -1632,14 +1660,29 @@ __global__ __launch_bounds__(256) void chunk_tb_kernel(Src<bf16_bits> qs, Src<bf
         for (int r = 0; r < 4; ++r) sh.mm[16 * wave + 4 * lk + r][j] = 0.f;
         continue;
       }
-      bf16x8 kcol[4];
+      bf16x8 kcol[kHalves][4];
 #pragma unroll
-      for (int n = 0; n < 4; ++n) kcol[n] = lds8(&sh.k[16 * tj + lr][32 * n + 8 * lk]);
+      for (int hl = 0; hl < kHalves; ++hl)
+#pragma unroll
+        for (int n = 0; n < 4; ++n) kcol[hl][n] = lds8(&sh.k[hl][16 * tj + lr][32 * n + 8 * lk]);
       floatx4 aa = floatx4{}, am = floatx4{};
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
-        aa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(krow[n], kcol[n], aa, 0, 0, 0);
-        am = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qrow[n], kcol[n], am, 0, 0, 0);
+        aa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(krow[0][n], kcol[0][n], aa, 0, 0, 0);
+        am = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qrow[0][n], kcol[0][n], am, 0, 0, 0);
+      }
+      if constexpr (kSplit) {
+        // hi*lo and lo*hi terms (lo*lo is below 2^-16 of the product).
+        floatx4 aa2 = floatx4{}, am2 = floatx4{};
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          aa2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(krow[0][n], kcol[kHalves - 1][n], aa2, 0, 0, 0);
+          am2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qrow[0][n], kcol[kHalves - 1][n], am2, 0, 0, 0);
+          aa2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(krow[kHalves - 1][n], kcol[0][n], aa2, 0, 0, 0);
+          am2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qrow[kHalves - 1][n], kcol[0][n], am2, 0, 0, 0);
+        }
+        aa += aa2;
+        am += am2;
       }
       const float gj = sh.g[j];
 #pragma unroll
@@ -1906,6 +1949,291 @@ __global__ __launch_bounds__(kTScanThreads) void chunk_tscan_kernel(Src<bf16_bit
   }
 }
 
+// ------------------------------ stage 2b, fp32 inputs as (hi, lo) planes
+// The full entry's q / k / v are fp32 convolution outputs, written as bf16
+// (hi, lo) planes (x = hi + lo); the scan is chunk_tscan_kernel's with every
+// product over q, k or v taken as hi*hi + hi*lo + lo*hi.  The planes double
+// the operand bytes, so only K (read in steps 1 and 3) is double-buffered;
+// Q and V are reloaded once step 1 has read them, Tb once step 2 has, and M
+// at the start of the chunk whose step 3 reads it.
+struct TScanSplitShared {
+  bf16_bits k[2][2][kChunk][kChunkDim]; // [chunk parity][hi, lo] K rows, 128-wide swizzle
+  bf16_bits q[2][kChunk][kChunkDim];    // [hi, lo] Q rows
+  bf16_bits tb[2][kChunk][kChunk];      // Tb (hi, lo), 64-wide swizzle
+  bf16_bits m[2][kChunk][kChunk];       // M (hi, lo)
+  bf16_bits v[2][kChunk][kColBlock];    // [hi, lo] V[i][c0 ..]
+  float g[2][kChunk];                   // [chunk parity] G
+  bf16_bits st[2][kColBlock][kLdK];
+  bf16_bits yt[2][kColBlock][kLdJ];
+  bf16_bits dt[2][kColBlock][kLdJ];
+  bf16_bits ft[2][kColBlock][kLdJ];
+  float qo[kChunk][kColBlock];
+};
+
+// LDS-direct loads of loader wave u = 0..3 (rows past L repeat row L-1):
+//   K: rows 16u .. +15 of both planes (8 instructions), and G (loader 2, one
+//      more);
+//   M, Tb: half u / 2, rows 32 (u % 2) .. +31 (4 each);
+//   Q: rows 16u .. +15 of both planes (8), V: plane u / 2, rows 32 (u % 2) ..
+//      +31 of this block's 16 columns (1).
+struct TScanSplitLoads {
+  static constexpr int kM = 4, kTb = 4, kQv = 9;
+  __device__ static constexpr int k_count(int u) { return 8 + (u == 2 ? 1 : 0); }
+  __device__ static void rows128(bf16_bits (*dst)[kChunkDim], const bf16_bits *base, std::size_t row,
+                                 int L, int u) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row0 = 16 * u + 4 * j, r = row0 + (lane >> 4), p = lane & 15;
+      const int src = r < L ? r : L - 1;
+      load_lds_b128(base, static_cast<std::uint32_t>(src * row * 2 + (p ^ (r & 15)) * 16),
+                    lds_address(&dst[row0][0]));
+    }
+  }
+  __device__ static void k(TScanSplitShared &sh, int parity, const Src<bf16_bits> &ks, std::size_t lo_plane,
+                           const unsigned char *record, std::size_t t0, int L, std::size_t kh, int u) {
+    const bf16_bits *kb = ks.base + t0 * ks.row + kh * ks.head_stride;
+    rows128(sh.k[parity][0], kb, ks.row, L, u);
+    rows128(sh.k[parity][1], kb + lo_plane, ks.row, L, u);
+    if (u == 2 && (threadIdx.x & 63) < 16)
+      load_lds_b128(record, static_cast<std::uint32_t>(rec2::kG + 16 * (threadIdx.x & 63)),
+                    lds_address(&sh.g[parity][0]));
+  }
+  __device__ static void m(TScanSplitShared &sh, const unsigned char *record, int u) {
+    const int half = u >> 1;
+    load_rows_lds<kChunk, kChunk, 32, 1>(record, static_cast<std::uint32_t>(rec2::kM + half * kChunk * kChunk * 2),
+                                         &sh.m[half], 32 * (u & 1));
+  }
+  __device__ static void tb(TScanSplitShared &sh, const unsigned char *record, int u) {
+    const int half = u >> 1;
+    load_rows_lds<kChunk, kChunk, 32, 1>(record, static_cast<std::uint32_t>(rec2::kTb + half * kChunk * kChunk * 2),
+                                         &sh.tb[half], 32 * (u & 1));
+  }
+  __device__ static void qv(TScanSplitShared &sh, const Src<bf16_bits> &qs, const Src<bf16_bits> &vs,
+                            std::size_t lo_plane, std::size_t t0, int L, std::size_t h, std::size_t kh, int c0,
+                            int u) {
+    const bf16_bits *qb = qs.base + t0 * qs.row + kh * qs.head_stride;
+    rows128(sh.q[0], qb, qs.row, L, u);
+    rows128(sh.q[1], qb + lo_plane, qs.row, L, u);
+    const int lane = threadIdx.x & 63;
+    const int row = 32 * (u & 1) + (lane >> 1), src = row < L ? row : L - 1;
+    const bf16_bits *vb = vs.base + t0 * vs.row + h * vs.head_stride + c0 + (u >> 1) * lo_plane;
+    load_lds_b128(vb, static_cast<std::uint32_t>(src * vs.row * 2 + (lane & 1) * 16),
+                  lds_address(&sh.v[u >> 1][32 * (u & 1)][0]));
+  }
+  // Waits until at most `later` of this wave's loads are outstanding (loads
+  // return in order).  The count must be an immediate, hence the branches.
+  template <int kFixed> __device__ static void wait_k_later(int u, bool more) {
+    if (!more)
+      wait_vm<kFixed>();
+    else if (u == 2)
+      wait_vm<kFixed + 9>();
+    else
+      wait_vm<kFixed + 8>();
+  }
+};
+
+template <typename OutT>
+__global__ __launch_bounds__(kTScanThreads) void chunk_tscan_split_kernel(Src<bf16_bits> qs, Src<bf16_bits> ks,
+                                                                          Src<bf16_bits> vs, std::size_t lo_plane,
+                                                                          ChunkScratch scratch,
+                                                                          float *__restrict__ state,
+                                                                          OutT *__restrict__ out,
+                                                                          std::size_t tokens, std::size_t hk,
+                                                                          std::size_t hv) {
+  using Loads = TScanSplitLoads;
+  __shared__ TScanSplitShared sh;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lk = lane >> 4;
+  const int u = wave - 4; // loader index of waves 4-7
+  const std::size_t h = blockIdx.x;
+  const std::size_t kh = h % hk;
+  const int c0 = blockIdx.y * kColBlock;
+  const float q_scale = qs.scale, k_scale = ks.scale, v_scale = vs.scale;
+  float *sg = state + h * kChunkDim * kChunkDim;
+  if (wave >= 4) {
+    const int L0 = static_cast<int>(tokens < kChunk ? tokens : kChunk);
+    const unsigned char *rec0 = scratch.at(h, 0);
+    Loads::k(sh, 0, ks, lo_plane, rec0, 0, L0, kh, u);
+    Loads::m(sh, rec0, u);
+    Loads::qv(sh, qs, vs, lo_plane, 0, L0, h, kh, c0, u);
+    Loads::tb(sh, rec0, u);
+  }
+  floatx4 s[2];
+  if (wave < 4) {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[tt][r] = sg[(32 * wave + 16 * tt + 4 * lk + r) * kChunkDim + c0 + lr];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) store_split_t<kLdK>(sh.st[0], sh.st[1], 32 * wave + 16 * tt, s[tt]);
+  }
+  floatx4 pend_o = floatx4{};
+  std::size_t pend_t0 = 0;
+  int pend_l = 0;
+  auto store_o = [&](std::size_t ot0, int ol) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * (wave & 3) + 4 * lk + r;
+      if (i < ol) Elem<OutT>::store(out, ((ot0 + i) * hv + h) * kChunkDim + c0 + lr, pend_o[r]);
+    }
+  };
+  const int rt = wave & 3, i0 = 16 * rt;
+  for (std::size_t c = 0, t0 = 0; t0 < tokens; ++c, t0 += kChunk) {
+    const int L = static_cast<int>(tokens - t0 < kChunk ? tokens - t0 : kChunk);
+    const int par = static_cast<int>(c & 1);
+    const bool more = t0 + kChunk < tokens;
+    const std::size_t t1 = t0 + kChunk;
+    const int L1 = more ? static_cast<int>(tokens - t1 < kChunk ? tokens - t1 : kChunk) : 0;
+    // K, G, Q, V of chunk c are in (Tb of chunk c, 4 loads, was issued later).
+    if (wave >= 4) {
+      if (c == 0)
+        wait_vm<0>();
+      else
+        wait_vm<Loads::kTb>();
+    }
+    __syncthreads();
+    if (wave >= 4) {
+      store_o(pend_t0, pend_l); // chunk c - 1
+      if (more) Loads::k(sh, par ^ 1, ks, lo_plane, scratch.at(h, c + 1), t1, L1, kh, u);
+      if (c > 0) Loads::m(sh, scratch.at(h, c), u); // step 3 of chunk c - 1 has read M
+    }
+    const float *g = sh.g[par];
+    const float glast = g[kChunk - 1];
+    // ---- 1
+    if (wave < 4) {
+      const bf16_bits *kh0 = &sh.k[par][0][0][0], *kh1 = &sh.k[par][1][0][0];
+      floatx4 x0 = floatx4{}, x1 = floatx4{}, x2 = floatx4{}, q0 = floatx4{}, q1 = floatx4{}, q2 = floatx4{};
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const int ro = swz128(i0 + lr, 4 * n + lk);
+        const bf16x8 kh = lds8(kh0 + ro), kl = lds8(kh1 + ro);
+        const bf16x8 qh = lds8(&sh.q[0][0][0] + ro), ql = lds8(&sh.q[1][0][0] + ro);
+        const bf16x8 sth = lds8(&sh.st[0][lr][32 * n + 8 * lk]), stl = lds8(&sh.st[1][lr][32 * n + 8 * lk]);
+        x0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, sth, x0, 0, 0, 0);
+        x1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, stl, x1, 0, 0, 0);
+        x2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, sth, x2, 0, 0, 0);
+        q0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh, sth, q0, 0, 0, 0);
+        q1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh, stl, q1, 0, 0, 0);
+        q2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql, sth, q2, 0, 0, 0);
+      }
+      floatx4 y, o;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = i0 + 4 * lk + r;
+        const float eg = __expf(g[i]);
+        const float vv = bf16_lo(sh.v[0][i][lr]) + bf16_lo(sh.v[1][i][lr]);
+        y[r] = v_scale * vv - eg * k_scale * (x0[r] + (x1[r] + x2[r]));
+        o[r] = eg * q_scale * (q0[r] + (q1[r] + q2[r]));
+      }
+      store_split_t<kLdJ>(sh.yt[0], sh.yt[1], i0, y);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sh.qo[i0 + 4 * lk + r][lr] = o[r];
+    }
+    // Tb of chunk c: issued before the K of chunk c + 1 and this chunk's M.
+    if (wave >= 4 && c > 0) {
+      if (more) {
+        if (u == 2)
+          wait_vm<Loads::kM + 9>();
+        else
+          wait_vm<Loads::kM + 8>();
+      } else {
+        wait_vm<Loads::kM>();
+      }
+    }
+    __syncthreads();
+    if (wave >= 4 && more) Loads::qv(sh, qs, vs, lo_plane, t1, L1, h, kh, c0, u); // step 1 has read Q, V
+    // ---- 2
+    if (wave < 4) {
+      floatx4 fdec;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) fdec[r] = __expf(glast - g[i0 + 4 * lk + r]);
+      floatx4 d0 = floatx4{}, d1 = floatx4{}, d2 = floatx4{};
+      const int steps = rt < 2 ? 1 : 2;
+      for (int n = 0; n < steps; ++n) {
+        const int to = swz64(i0 + lr, 4 * n + lk);
+        const bf16x8 th = lds8(&sh.tb[0][0][0] + to), tl = lds8(&sh.tb[1][0][0] + to);
+        const bf16x8 yh = lds8(&sh.yt[0][lr][32 * n + 8 * lk]), yl = lds8(&sh.yt[1][lr][32 * n + 8 * lk]);
+        d0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(th, yh, d0, 0, 0, 0);
+        d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(th, yl, d1, 0, 0, 0);
+        d2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tl, yh, d2, 0, 0, 0);
+      }
+      floatx4 dv, fv;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = i0 + 4 * lk + r;
+        dv[r] = d0[r] + (d1[r] + d2[r]);
+        fv[r] = (i < L ? 1.f : 0.f) * (fdec[r] * dv[r]);
+      }
+      store_split_t<kLdJ>(sh.dt[0], sh.dt[1], i0, dv);
+      store_split_t<kLdJ>(sh.ft[0], sh.ft[1], i0, fv);
+    }
+    // M of chunk c: only this chunk's Q and V (if any) were issued after it.
+    if (wave >= 4 && c > 0) {
+      if (more)
+        wait_vm<Loads::kQv>();
+      else
+        wait_vm<0>();
+    }
+    __syncthreads();
+    if (wave >= 4 && more) Loads::tb(sh, scratch.at(h, c + 1), u); // step 2 has read Tb
+    // ---- 3
+    if (wave < 4) {
+      const bf16_bits *kh0 = &sh.k[par][0][0][0], *kh1 = &sh.k[par][1][0][0];
+      const float egl = __expf(glast);
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int d0 = 32 * wave + 16 * tt;
+        const int dsrc = d0 + 4 * (lr & 3);
+        floatx4 a0 = floatx4{}, a1 = floatx4{}, a2 = floatx4{};
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+          u32x2 ph[2], pl[2];
+#pragma unroll
+          for (int hq = 0; hq < 2; ++hq) {
+            const int j = 32 * n + 8 * lk + 4 * hq + (lr >> 2);
+            const int off = swz128(j, dsrc >> 3) + (dsrc & 7);
+            ph[hq] = lds_tr16_b64(kh0 + off);
+            pl[hq] = lds_tr16_b64(kh1 + off);
+          }
+          const bf16x8 kth = __builtin_bit_cast(bf16x8, u32x4{ph[0][0], ph[0][1], ph[1][0], ph[1][1]});
+          const bf16x8 ktl = __builtin_bit_cast(bf16x8, u32x4{pl[0][0], pl[0][1], pl[1][0], pl[1][1]});
+          const bf16x8 fh = lds8(&sh.ft[0][lr][32 * n + 8 * lk]), fl = lds8(&sh.ft[1][lr][32 * n + 8 * lk]);
+          a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kth, fh, a0, 0, 0, 0);
+          a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kth, fl, a1, 0, 0, 0);
+          a2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ktl, fh, a2, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s[tt][r] = fmaf(egl, s[tt][r], k_scale * (a0[r] + (a1[r] + a2[r])));
+        store_split_t<kLdK>(sh.st[0], sh.st[1], d0, s[tt]);
+      }
+    } else {
+      floatx4 m0 = floatx4{}, m1 = floatx4{}, m2 = floatx4{};
+      const int steps = rt < 2 ? 1 : 2;
+      for (int n = 0; n < steps; ++n) {
+        const int mo = swz64(i0 + lr, 4 * n + lk);
+        const bf16x8 mh = lds8(&sh.m[0][0][0] + mo), ml = lds8(&sh.m[1][0][0] + mo);
+        const bf16x8 dh = lds8(&sh.dt[0][lr][32 * n + 8 * lk]), dl = lds8(&sh.dt[1][lr][32 * n + 8 * lk]);
+        m0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mh, dh, m0, 0, 0, 0);
+        m1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mh, dl, m1, 0, 0, 0);
+        m2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ml, dh, m2, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pend_o[r] = sh.qo[i0 + 4 * lk + r][lr] + (m0[r] + (m1[r] + m2[r]));
+      pend_t0 = t0;
+      pend_l = L;
+    }
+  }
+  if (wave >= 4) store_o(pend_t0, pend_l);
+  if (wave < 4) {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sg[(32 * wave + 16 * tt + 4 * lk + r) * kChunkDim + c0 + lr] = s[tt][r];
+  }
+}
+
 // ----------------------------------------------------- stage 3 kernel
 // Block (token, value head): RMSNorm over dv, x weight, x SiLU(z)
 // (cpp/kernels/qwen35_delta.cu:578-621).
@@ -1943,7 +2271,7 @@ void launch_recurrence(Src<InT> q, Src<InT> k, Src<InT> v, const float *beta, co
     const dim3 pgrid{static_cast<unsigned>(hv), static_cast<unsigned>(ceil_div_unchecked(tokens, kChunk)), 1};
     const dim3 sgrid{static_cast<unsigned>(hv), kChunkDim / kColBlock, 1};
     if constexpr (std::is_same_v<InT, bf16_bits>) {
-      chunk_tb_kernel<<<pgrid, 256, 0, stream>>>(q, k, beta, g, scratch, tokens, hk, hv);
+      chunk_tb_kernel<false><<<pgrid, 256, 0, stream>>>(q, k, 0, beta, g, scratch, tokens, hk, hv);
       check_launch<Err>("qwen35_gated_delta chunk preparation");
       chunk_tscan_kernel<OutT><<<sgrid, kTScanThreads, 0, stream>>>(q, k, v, scratch, state, out, tokens, hk, hv);
       check_launch<Err>("qwen35_gated_delta chunk scan");
@@ -2021,6 +2349,10 @@ void launch_typed(const DeltaSources &src, const void *conv_weight, const void *
                               reinterpret_cast<std::uintptr_t>(conv_state)) & 15u) == 0;
   const bool chunked = use_chunked(s, policy) && (reinterpret_cast<std::uintptr_t>(ws) & 15u) == 0;
   const bool one_token_state = wide && s.tokens == 1;
+  // The chunked path on the wide convolution takes q / k / v as (hi, lo)
+  // bf16 planes (chunk_tb_kernel<true> + chunk_tscan_split_kernel).
+  const bool split_chunked = wide && chunked && !one_token_state && s.key_dim == kChunkDim &&
+                             s.value_dim == kChunkDim;
   constexpr int kConvTokens = 4; // tokens per workgroup of the multi-token convolution
   if (wide) {
     const unsigned blocks_y = static_cast<unsigned>(c.conv_dim / kConvWideChannels);
@@ -2029,6 +2361,13 @@ void launch_typed(const DeltaSources &src, const void *conv_weight, const void *
           in, static_cast<const Wt *>(conv_weight), conv_state, static_cast<const Wt *>(recurrent_a),
           static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, s.tokens,
           c.conv_dim, 2 * c.key_size, s.value_heads);
+    else if (split_chunked)
+      conv_norm_wide_kernel<T, Wt, 4, kConvTokens, false, true>
+          <<<dim3(static_cast<unsigned>(ceil_div_unchecked(s.tokens, kConvTokens)), blocks_y, 1), 64, 0,
+             stream>>>(
+              in, static_cast<const Wt *>(conv_weight), conv_state, static_cast<const Wt *>(recurrent_a),
+              static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, s.tokens,
+              c.conv_dim, 2 * c.key_size, s.value_heads);
     else
       conv_norm_wide_kernel<T, Wt, 4, kConvTokens, false>
           <<<dim3(static_cast<unsigned>(ceil_div_unchecked(s.tokens, kConvTokens)), blocks_y, 1), 64, 0,
@@ -2068,9 +2407,27 @@ void launch_typed(const DeltaSources &src, const void *conv_weight, const void *
     check_launch<Err>("qwen35_gated_delta register recurrent update");
     return;
   }
-  launch_recurrence<float, float>(q, k, v, beta, gdecay, rec_state, raw, scratch, s.tokens,
-                                  s.key_heads, s.value_heads, s.key_dim, s.value_dim, chunked,
-                                  stream);
+  if (split_chunked) {
+    const bf16_bits *planes = reinterpret_cast<const bf16_bits *>(convolved);
+    const Src<bf16_bits> qh{planes, c.conv_dim, s.key_dim, 1.0f};
+    const Src<bf16_bits> kh{planes + c.key_size, c.conv_dim, s.key_dim, 1.0f};
+    const Src<bf16_bits> vh{planes + 2 * c.key_size, c.conv_dim, s.value_dim, 1.0f};
+    const std::size_t lo_plane = s.tokens * c.conv_dim;
+    ChunkScratch rec = scratch;
+    rec.bytes = rec2::kBytes;
+    const dim3 pgrid{static_cast<unsigned>(s.value_heads), static_cast<unsigned>(rec.chunks), 1};
+    chunk_tb_kernel<true><<<pgrid, 256, 0, stream>>>(qh, kh, lo_plane, beta, gdecay, rec, s.tokens, s.key_heads,
+                                                     s.value_heads);
+    check_launch<Err>("qwen35_gated_delta chunk preparation");
+    const dim3 sgrid{static_cast<unsigned>(s.value_heads), kChunkDim / kColBlock, 1};
+    chunk_tscan_split_kernel<float><<<sgrid, kTScanThreads, 0, stream>>>(qh, kh, vh, lo_plane, rec, rec_state, raw,
+                                                                         s.tokens, s.key_heads, s.value_heads);
+    check_launch<Err>("qwen35_gated_delta chunk scan");
+  } else {
+    launch_recurrence<float, float>(q, k, v, beta, gdecay, rec_state, raw, scratch, s.tokens,
+                                    s.key_heads, s.value_heads, s.key_dim, s.value_dim, chunked,
+                                    stream);
+  }
   if (fast)
     out_norm_fast_kernel<T, Wt><<<static_cast<unsigned>(s.tokens), 256, 0, stream>>>(
         in, static_cast<const Wt *>(norm_w), raw, static_cast<T *>(output), c.conv_dim,
