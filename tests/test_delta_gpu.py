@@ -122,7 +122,8 @@ def model_shape(T):
     return dict(tokens=T, hidden=4096, hk=16, hv=32, dk=128, dv=128, width=4, eps=1e-6)
 
 
-@pytest.mark.parametrize("T,schedule", [(3, 0), (2, 0), (1, 2), (1, 0), (17, 1), (128, 0), (150, 0)])
+@pytest.mark.parametrize("T,schedule", [(3, 0), (2, 0), (1, 2), (1, 0), (17, 1), (64, 0), (128, 0), (150, 0),
+                                        (257, 0)])
 def test_model_shape_schedules(gpu, T, schedule):
     # cpp/tests/qwen35_cuda_delta_test.cu:631-650 plus both gfx950 schedules.
     sh = model_shape(T)
@@ -139,8 +140,8 @@ def test_model_shape_schedules(gpu, T, schedule):
 @pytest.mark.parametrize("dt,wdt", [(1, 1), (2, 2), (1, 3)])
 def test_model_shape_chunked_f32_f16_activations(gpu, dt, wdt):
     # The chunked path (T >= 64, two chunks with a ragged tail) with f32 / f16 activations and
-    # f32 or bf16 auxiliary weights: these go through the f32 chunk prep and the hi/lo
-    # (inexact) scan.
+    # f32 or bf16 auxiliary weights: the convolution writes q / k / v as (hi, lo) bf16 planes
+    # and the T-record prep and split scan take every product over them in three parts.
     T = 100
     sh = model_shape(T)
     fx = fixture_for(sh, seed=T + dt)
