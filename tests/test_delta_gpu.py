@@ -210,6 +210,32 @@ def test_core_chunked_ragged_lengths_with_state(gpu, T):
     assert_bf16_close(got_o, bf16(want_o), what=f"chunked core T={T}")
 
 
+@pytest.mark.parametrize("hk,hv", [(8, 32), (32, 32), (4, 8)])
+def test_core_chunked_head_groupings(gpu, hk, hv):
+    """Value head h reads key head h % Hk; the chunk kernels index K and Q
+    rows by it, so other groupings than 16 / 32 must hold too."""
+    T = 100
+    r = rng(300 + hk)
+    q, k = normal(r, T, hk, 128), normal(r, T, hk, 128)
+    q = bf16(q / np.linalg.norm(q, axis=-1, keepdims=True))
+    k = bf16(k / np.linalg.norm(k, axis=-1, keepdims=True))
+    v = bf16(normal(r, T, hv, 128))
+    beta = (1 / (1 + np.exp(-normal(r, T, hv)))).astype(np.float32)
+    g = (-np.log1p(np.exp(normal(r, T, hv)))).astype(np.float32)
+    s0 = normal(r, hv, 128, 128, scale=0.05)
+    want_o, want_s = orc.delta_core(q, k, v, beta, g, 1 / np.sqrt(128), s0)
+    st = to_dev(s0, torch.float32)
+    out = torch.empty(T, hv, 128, device="cuda", dtype=torch.bfloat16)
+    ws = torch.empty(ops.qwen35_gated_delta_core_workspace_bytes(T, hk, hv, 128, 128), device="cuda",
+                     dtype=torch.uint8)
+    bt = lambda a: to_dev(a, torch.bfloat16)
+    ops.qwen35_gated_delta_core(bt(q), bt(k), bt(v), to_dev(beta, torch.float32), to_dev(g, torch.float32),
+                                1 / np.sqrt(128), st, out, ws, True)
+    torch.cuda.synchronize()
+    assert rel_l2(from_dev(st), want_s) < 1e-4
+    assert_bf16_close(from_dev(out), bf16(want_o), what=f"chunked core hk={hk} hv={hv}")
+
+
 def test_core_chunked_equals_recurrent(gpu):
     T = 200
     q, k, v, beta, g = cfg5_inputs(T, 7)
