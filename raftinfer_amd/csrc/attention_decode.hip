@@ -12,6 +12,7 @@
 #include "raftinfer_amd/qwen35_online_attention.hpp"
 
 #include <atomic>
+#include <type_traits>
 #include <cmath>
 #include <mutex>
 
@@ -478,13 +479,14 @@ __device__ __forceinline__ void append_rows_fused(const DecodeMfmaArgs &a, const
 // gate: element (head h, dim d) at gate[h * gate_stride + d] (gate_stride 256
 // for a split gate, 512 for the gate half of a q projection row).
 // Single-block workgroup `block` at `position` (ctx = position + 1).
-template <int DS, int WAVES, bool kFused>
+template <int DS, int WAVES, bool kFused, bool kDma = false>
 __device__ __forceinline__ void single_block_body(unsigned block, const DecodeMfmaArgs &a,
                                                   const bf16_bits *__restrict__ gate,
                                                   std::size_t gate_stride,
                                                   bf16_bits *__restrict__ output,
                                                   std::size_t position, const FusedNormRope &f,
-                                                  DecodeMfmaShared<DS, WAVES> &sh, DecodeFusedQK &fq) {
+                                                  DecodeMfmaShared<DS, WAVES> &sh, DecodeFusedQK &fq,
+                                                  DecodeStage<DS, WAVES> *stage = nullptr) {
   constexpr int DIMS = kHeadDim / DS;
   const std::size_t ctx = position + 1;
   std::size_t kv_head;
@@ -493,17 +495,26 @@ __device__ __forceinline__ void single_block_body(unsigned block, const DecodeMf
   if (kv_head >= kKvHeads) return;
   // The gate values of this thread's outputs are loaded before the scan, so
   // the epilogue does not wait for a load round trip of its own.
+  // kDma: unconditional (index clamped) with the raw bits kept until the
+  // epilogue, since a conditional load converted on the spot is waited for
+  // right here, before the stage loads go out.
   constexpr int kOut = (kGroup * DIMS + WAVES * 64 - 1) / (WAVES * 64);
   float gv[kOut];
+  [[maybe_unused]] bf16_bits graw[kOut];
 #pragma unroll
   for (int n = 0; n < kOut; ++n) {
     const int o = threadIdx.x + n * WAVES * 64;
-    gv[n] = 0.f;
-    if (o < kGroup * DIMS)
-      gv[n] = bf16_to_f32(gate[(kv_head * kGroup + o / DIMS) * gate_stride + dq * DIMS + o % DIMS]);
+    if constexpr (kDma) {
+      const int oc = o < kGroup * DIMS ? o : kGroup * DIMS - 1;
+      graw[n] = gate[(kv_head * kGroup + oc / DIMS) * gate_stride + dq * DIMS + oc % DIMS];
+    } else {
+      gv[n] = 0.f;
+      if (o < kGroup * DIMS)
+        gv[n] = bf16_to_f32(gate[(kv_head * kGroup + o / DIMS) * gate_stride + dq * DIMS + o % DIMS]);
+    }
   }
   if constexpr (kFused) fused_qk_prologue(f, kv_head, position, fq);
-  decode_mfma_scan<DS, WAVES, 32, kFused>(a, kv_head, dq, 0, ctx, position, sh, &fq);
+  decode_mfma_scan<DS, WAVES, 32, kFused, kDma>(a, kv_head, dq, 0, ctx, position, sh, &fq, stage);
   __syncthreads();
   // The scan read the new row from key/value; the cache copy goes last so its
   // load latency is not on the critical path.
@@ -521,21 +532,29 @@ __device__ __forceinline__ void single_block_body(unsigned block, const DecodeMf
     float mm, l, acc;
     decode_mfma_combine(sh, h, d, mm, l, acc);
     const std::size_t idx = (kv_head * kGroup + h) * kHeadDim + dq * DIMS + d;
+    if constexpr (kDma) gv[n] = bf16_to_f32(graw[n]);
     output[idx] = f32_to_bf16((acc / l) * sigmoid_gate(gv[n]));
   }
 }
 
-template <int DS, int WAVES, bool kFused = false>
+// kDma: K and V reach the scan through an LDS stage (DecodeStage, 146 KiB).
+template <int DS, int WAVES, bool kFused = false, bool kDma = false>
 __global__ __launch_bounds__(WAVES * 64) void decode_single_mfma_kernel(
     DecodeMfmaArgs a, const bf16_bits *__restrict__ gate, std::size_t gate_stride,
     bf16_bits *__restrict__ output, std::size_t host_position, const std::uint32_t *device_position,
     std::size_t threshold, FusedNormRope f) {
   __shared__ DecodeMfmaShared<DS, WAVES> sh;
   __shared__ DecodeFusedQK fq;
+  using Stage = std::conditional_t<kDma, DecodeStage<DS, WAVES>, char>;
+  __shared__ Stage stage;
   const std::size_t position = read_position(device_position, host_position);
   if (position >= a.max_ctx) return;
   if (threshold != 0 && position + 1 >= threshold) return;
-  single_block_body<DS, WAVES, kFused>(blockIdx.x, a, gate, gate_stride, output, position, f, sh, fq);
+  if constexpr (kDma)
+    single_block_body<DS, WAVES, kFused, true>(blockIdx.x, a, gate, gate_stride, output, position, f, sh, fq,
+                                               &stage);
+  else
+    single_block_body<DS, WAVES, kFused, false>(blockIdx.x, a, gate, gate_stride, output, position, f, sh, fq);
 }
 
 // Split-K partition workgroup `block` at `position`.
@@ -709,10 +728,20 @@ void launch_decode_mfma(const DecodeMfmaArgs &args, const bf16_bits *g, std::siz
     return;
   }
   if (!partition_only && (dynamic || single || host_ctx < plan.split_k_threshold_tokens)) {
-    decode_single_mfma_kernel<kSingleDs, kSingleMfmaWaves, kFused>
-        <<<xcd_grid<kSingleDs>(kKvHeads), kSingleMfmaWaves * 64, 0, stream>>>(
-            args, g, gate_stride, out, shape.past_tokens, device_position,
-            plan.split_k_threshold_tokens, f);
+    // Above two chunks per wave the LDS-staged scan streams the next chunk
+    // under the current one (ctx 1024: 11.2 -> 10.3 us hot); at ctx <= 512
+    // the register-fed scan is as fast or faster cold.
+    const std::size_t ctx_bound = dynamic ? shape.max_context_tokens : host_ctx;
+    if (ctx_bound > 2 * kSingleMfmaWaves * 32)
+      decode_single_mfma_kernel<kSingleDs, kSingleMfmaWaves, kFused, true>
+          <<<xcd_grid<kSingleDs>(kKvHeads), kSingleMfmaWaves * 64, 0, stream>>>(
+              args, g, gate_stride, out, shape.past_tokens, device_position,
+              plan.split_k_threshold_tokens, f);
+    else
+      decode_single_mfma_kernel<kSingleDs, kSingleMfmaWaves, kFused, false>
+          <<<xcd_grid<kSingleDs>(kKvHeads), kSingleMfmaWaves * 64, 0, stream>>>(
+              args, g, gate_stride, out, shape.past_tokens, device_position,
+              plan.split_k_threshold_tokens, f);
     check_launch<Err>("qwen35_online_attention_decode_gfx950_hd256");
   }
   if (single || (!dynamic && host_ctx < plan.split_k_threshold_tokens)) return;

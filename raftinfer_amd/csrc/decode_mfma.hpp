@@ -48,6 +48,19 @@ template <int DS, int WAVES, int CT = 32> struct DecodeMfmaShared {
   float acc[WAVES][4][DIMS];
 };
 
+// LDS stage of the DMA-fed scan: per wave, one chunk's K rows (16-byte piece
+// c of row t at piece c ^ (2 * (t % 8)), so the score reads of 8 tokens x 2
+// pieces hit distinct banks) and its V slice.
+template <int DS, int WAVES, int CT = 32> struct DecodeStage {
+  alignas(16) unsigned char k[WAVES][CT * kHeadDim * 2];
+  alignas(16) bf16_bits v[WAVES][CT * (kHeadDim / DS)];
+  // q of the GQA group and the new token's K and V rows (each row twice: one
+  // load instruction moves 1 KiB), written alike by every wave.
+  alignas(16) bf16_bits q[kGroup][kHeadDim];
+  alignas(16) bf16_bits knew[2][kHeadDim];
+  alignas(16) bf16_bits vnew[2][kHeadDim];
+};
+
 // PV lane mapping for a DIMS-wide slice and CT-token chunks: a lane owns VEC
 // consecutive dims (one 2*VEC-byte load per token) and one of TL token phases.
 template <int DIMS, int CT = 32> struct PvMap {
@@ -101,11 +114,12 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 //
 // kFused: q comes from fq->q and the new token's key row from fq->k (both in
 // LDS) instead of a.query and a.key_new.
-template <int DS, int WAVES, int CT = 32, bool kFused = false>
+template <int DS, int WAVES, int CT = 32, bool kFused = false, bool kDma = false>
 __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::size_t kv_head,
                                                  int dq, std::size_t begin, std::size_t end,
                                                  std::size_t pos, DecodeMfmaShared<DS, WAVES, CT> &sh,
-                                                 const DecodeFusedQK *fq = nullptr) {
+                                                 const DecodeFusedQK *fq = nullptr,
+                                                 DecodeStage<DS, WAVES, CT> *stage = nullptr) {
   constexpr int DIMS = kHeadDim / DS;
   constexpr int G = CT / 8; // 8-token groups per chunk
   // K is read non-temporally when at most 4 sibling workgroups share it
@@ -128,13 +142,65 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
   const bf16_bits *kplane = a.cache;
   const bf16_bits *vplane = a.cache + plane;
 
+  // kDma: the chunk's K rows and V slice go straight to this wave's LDS
+  // stage (global_load_lds_dwordx4) and are read back before the next
+  // chunk's loads are issued into the same place, so the next chunk streams
+  // in while this one is used.  Rows past `end` read row end-1.  Every load of
+  // the scan goes through the stage (q and the new token's rows too), so all
+  // its waits are counted by hand and the compiler places none of its own
+  // between them.
+  [[maybe_unused]] unsigned k_lds = 0, v_lds = 0;
+  // Half h of a chunk: K rows 16h .. 16h+15 (8 instructions), and for h = 1
+  // also the V slice of all 32 rows (1 instruction).
+  auto dma_half = [&](std::size_t c0, int h) {
+    const bf16_bits *kb = kplane + cache_row(a.head_major, c0, kv_head, a.max_ctx);
+    const std::size_t row_elems = a.head_major ? kHeadDim : kKvHeads * kHeadDim;
+#pragma unroll
+    for (int jj = 0; jj < CT / 4; ++jj) {
+      const int j = (CT / 4) * h + jj;
+      const int r = 2 * j + (lane >> 5);
+      const std::size_t tok = c0 + r < end ? c0 + r : end - 1;
+      const std::uint32_t voff = static_cast<std::uint32_t>((tok - c0) * row_elems * 2) +
+                                 16u * static_cast<std::uint32_t>((lane & 31) ^ (2 * (r & 7)));
+      load_lds_b128(kb, voff, k_lds + 1024u * j);
+    }
+    if (h == 1) {
+      const bf16_bits *vb = vplane + cache_row(a.head_major, c0, kv_head, a.max_ctx) + dq * DIMS;
+      const int r = lane / (64 / CT);
+      const std::size_t tok = c0 + r < end ? c0 + r : end - 1;
+      load_lds_b128(vb, static_cast<std::uint32_t>((tok - c0) * row_elems * 2) + 16u * (lane % (64 / CT)),
+                    v_lds);
+    }
+  };
+  if constexpr (kDma) {
+    static_assert(CT == 32 && DIMS * 2 * CT == 1024 && VEC == 2, "one V instruction per chunk");
+    k_lds = lds_address(&stage->k[wave][0]);
+    v_lds = lds_address(&stage->v[wave][0]);
+    const std::uint32_t row_off = 16u * static_cast<std::uint32_t>(lane & 31);
+    if constexpr (!kFused) {
+      load_lds_b128(a.query + kv_head * kGroup * kHeadDim, 16u * lane, lds_address(&stage->q[0][0]));
+      load_lds_b128(a.query + kv_head * kGroup * kHeadDim, 1024u + 16u * lane, lds_address(&stage->q[2][0]));
+      load_lds_b128(a.key_new + kv_head * kHeadDim, row_off, lds_address(&stage->knew[0][0]));
+    }
+    load_lds_b128(a.value_new + kv_head * kHeadDim, row_off, lds_address(&stage->vnew[0][0]));
+    if (begin + static_cast<std::size_t>(wave) * CT < end) {
+      dma_half(begin + static_cast<std::size_t>(wave) * CT, 0);
+      dma_half(begin + static_cast<std::size_t>(wave) * CT, 1);
+      wait_vm<CT / 2 + 1>(); // q and the new rows have landed
+    } else {
+      wait_vm<0>();
+    }
+  }
+
   // B operand per line: column n < 8 = (half' = n/4, head n%4).
   bf16x8 qb[4];
 #pragma unroll
   for (int line = 0; line < 4; ++line) {
     u32x4 w = u32x4{0u, 0u, 0u, 0u};
     if (n < 8) {
-      if constexpr (kFused)
+      if constexpr (kDma && !kFused)
+        w = *reinterpret_cast<const u32x4 *>(&stage->q[n & 3][line * 64 + (2 * kq + (n >> 2)) * 8]);
+      else if constexpr (kFused)
         w = *reinterpret_cast<const u32x4 *>(&fq->q[n & 3][line * 64 + (2 * kq + (n >> 2)) * 8]);
       else
         w = *reinterpret_cast<const u32x4 *>(a.query + (kv_head * kGroup + (n & 3)) * kHeadDim + line * 64 +
@@ -153,41 +219,90 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
 
   for (std::size_t c0 = begin + static_cast<std::size_t>(wave) * CT; c0 < end;
        c0 += static_cast<std::size_t>(WAVES) * CT) {
-    // Issue every load of the chunk first: K for the scores, V for the slice.
-    // Tokens past `end` read row end-1 (in bounds); they are masked below.
     u32x4 kr[G][4];
+    VRow<VEC> vv[TPL];
+    if constexpr (kDma) {
+      // The stage is used in two halves so that the next chunk streams in
+      // behind this one: once rows 0-15 have landed and been read, the next
+      // chunk's rows 0-15 go out; then rows 16-31 and V, likewise.  Loads
+      // retire in order, so "at most 9 outstanding" means this chunk's first
+      // half has landed (its second half is the 9 youngest).
+      const bool more = c0 + static_cast<std::size_t>(WAVES) * CT < end; // wave-uniform
+      wait_vm<CT / 4 + 1>();
+      const unsigned char *kst = reinterpret_cast<const unsigned char *>(&stage->k[wave][0]);
+      auto read_groups = [&](int g0) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      std::size_t tok = c0 + 8 * g + rt;
-      tok = tok < end ? tok : end - 1;
-      // (fused: the cache row of the new token is read too, and replaced below)
-      const bf16_bits *row = !kFused && tok == pos ? a.key_new + kv_head * kHeadDim
-                                                   : kplane + cache_row(a.head_major, tok, kv_head, a.max_ctx);
+        for (int g = g0; g < g0 + G / 2; ++g) {
+          const int t = 8 * g + rt;
 #pragma unroll
-      for (int line = 0; line < 4; ++line)
-        kr[g][line] = kNtKeys ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(row + line * 64 + seg * 8))
-                              : *reinterpret_cast<const u32x4 *>(row + line * 64 + seg * 8);
-    }
-    if constexpr (kFused) {
+          for (int line = 0; line < 4; ++line)
+            kr[g][line] = *reinterpret_cast<const u32x4 *>(kst + t * 512 + 16 * ((line * 8 + seg) ^ (2 * (t & 7))));
+        }
+      };
+      read_groups(0);
+      wait_lgkm0(); // rows 0-15 have been read
+      if (more) {
+        dma_half(c0 + static_cast<std::size_t>(WAVES) * CT, 0);
+        wait_vm<CT / 4>(); // this chunk's second half has landed
+      } else {
+        wait_vm<0>();
+      }
+      read_groups(G / 2);
+#pragma unroll
+      for (int j = 0; j < TPL; ++j)
+        vv[j].w[0] = *reinterpret_cast<const std::uint32_t *>(&stage->v[wave][(tl + TL * j) * DIMS + VEC * dl]);
+      wait_lgkm0(); // rows 16-31 and V have been read
+      if (more) dma_half(c0 + static_cast<std::size_t>(WAVES) * CT, 1);
       if (pos >= c0 && pos < c0 + CT) { // this chunk holds the new token (wave-uniform)
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           if (c0 + 8 * g + rt == pos) {
 #pragma unroll
             for (int line = 0; line < 4; ++line)
-              kr[g][line] = *reinterpret_cast<const u32x4 *>(&fq->k[line * 64 + seg * 8]);
+              kr[g][line] = *reinterpret_cast<const u32x4 *>(
+                  kFused ? &fq->k[line * 64 + seg * 8] : &stage->knew[0][line * 64 + seg * 8]);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < TPL; ++j)
+          if (c0 + tl + TL * j == pos)
+            vv[j].w[0] = *reinterpret_cast<const std::uint32_t *>(&stage->vnew[0][dq * DIMS + VEC * dl]);
+      }
+    } else {
+      // Issue every load of the chunk first: K for the scores, V for the slice.
+      // Tokens past `end` read row end-1 (in bounds); they are masked below.
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        std::size_t tok = c0 + 8 * g + rt;
+        tok = tok < end ? tok : end - 1;
+        // (fused: the cache row of the new token is read too, and replaced below)
+        const bf16_bits *row = !kFused && tok == pos ? a.key_new + kv_head * kHeadDim
+                                                     : kplane + cache_row(a.head_major, tok, kv_head, a.max_ctx);
+#pragma unroll
+        for (int line = 0; line < 4; ++line)
+          kr[g][line] = kNtKeys ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(row + line * 64 + seg * 8))
+                                : *reinterpret_cast<const u32x4 *>(row + line * 64 + seg * 8);
+      }
+      if constexpr (kFused) {
+        if (pos >= c0 && pos < c0 + CT) { // this chunk holds the new token (wave-uniform)
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            if (c0 + 8 * g + rt == pos) {
+#pragma unroll
+              for (int line = 0; line < 4; ++line)
+                kr[g][line] = *reinterpret_cast<const u32x4 *>(&fq->k[line * 64 + seg * 8]);
+            }
           }
         }
       }
-    }
-    VRow<VEC> vv[TPL];
 #pragma unroll
-    for (int j = 0; j < TPL; ++j) {
-      std::size_t tok = c0 + tl + TL * j;
-      tok = tok < end ? tok : end - 1;
-      const bf16_bits *row = tok == pos ? a.value_new + kv_head * kHeadDim
-                                        : vplane + cache_row(a.head_major, tok, kv_head, a.max_ctx);
-      vv[j].load(row + dq * DIMS + VEC * dl);
+      for (int j = 0; j < TPL; ++j) {
+        std::size_t tok = c0 + tl + TL * j;
+        tok = tok < end ? tok : end - 1;
+        const bf16_bits *row = tok == pos ? a.value_new + kv_head * kHeadDim
+                                          : vplane + cache_row(a.head_major, tok, kv_head, a.max_ctx);
+        vv[j].load(row + dq * DIMS + VEC * dl);
+      }
     }
     // Keep every load of the chunk ahead of the first wait: the scheduler
     // otherwise sinks V loads below the K waits, adding a second round trip.

@@ -165,6 +165,21 @@ def test_split_k_cfg2_long_context(gpu, ctx):
     assert_bf16_close(out, bf16(expect), what=f"cfg2 ctx {ctx}")
 
 
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("ctx", [513, 777, 1024, 1500])
+def test_single_block_staged_scan(gpu, layout, ctx):
+    # Above 512 tokens the single-block kernel feeds its scan through an LDS
+    # stage (the next chunk streams in under the current one); ragged last
+    # chunks, both cache layouts, host and device positions.
+    for device_position in (False, True):
+        out, expect, cache, keys, vals, _, _ = run_decode(3, 1, layout, ctx, ctx + 7, mode=1,
+                                                          device_position=device_position,
+                                                          seed=ctx * 3 + layout, heavy_rows=0.01)
+        assert_bf16_close(out, bf16(expect), what=f"single-block ctx {ctx} layout {layout}")
+        ck, cv = read_cache(cache, layout, ctx, ctx + 7)
+        assert np.array_equal(ck, keys) and np.array_equal(cv, vals)
+
+
 def test_single_block_equals_split(gpu):
     a, *_ = run_decode(3, 1, 1, 1500, 2048, mode=1, seed=99)
     b, *_ = run_decode(3, 1, 1, 1500, 2048, mode=2, seed=99)

@@ -70,7 +70,7 @@ def _decode_case(ctx, max_ctx, mode, rot, wdt, layout, device_position, seed):
 
 @pytest.mark.parametrize("ctx,max_ctx,mode", [(100, 1024, ops.SPLIT_K_256), (300, 1024, ops.SPLIT_K_256),
                                               (4096, 4096, ops.AUTO), (512, 512, ops.SINGLE_BLOCK),
-                                              (1500, 2048, ops.SPLIT_K_512)])
+                                              (1000, 1024, ops.SINGLE_BLOCK), (1500, 2048, ops.SPLIT_K_512)])
 @pytest.mark.parametrize("device_position", [False, True])
 def test_fused_decode_equals_producers_then_decode(gpu, ctx, max_ctx, mode, device_position):
     c = _decode_case(ctx, max_ctx, mode, 64, torch.bfloat16, ops.HEAD_MAJOR, device_position,
