@@ -413,6 +413,23 @@ __global__ __launch_bounds__(64) void conv_norm_wide_kernel(
   static_assert(!kUpdateState || TT == 1, "the fused state update is for one-token calls");
   const std::size_t t0 = static_cast<std::size_t>(blockIdx.x) * TT;
   const std::size_t c = static_cast<std::size_t>(blockIdx.y) * kConvWideChannels + 8 * threadIdx.x;
+  // beta and the decay of the block's tokens: from an extra row of blocks
+  // past the channels when the grid has one (it then costs no other block a
+  // further round trip), else from the first block of channels.
+  auto beta_decay = [&]() {
+    for (int i = threadIdx.x; i < TT * static_cast<int>(hv); i += 64) {
+      const std::size_t t = t0 + i / hv, h = i % hv;
+      if (t >= tokens) break;
+      const float b = Elem<T>::load(in.b, t * in.b_stride + h);
+      const float a = Elem<T>::load(in.a, t * in.a_stride + h);
+      beta[t * hv + h] = sigmoid(b);
+      gdecay[t * hv + h] = Elem<Wt>::load(recurrent_a, h) * softplus(a + Elem<Wt>::load(dt_bias, h));
+    }
+  };
+  if (c >= conv_dim) {
+    beta_decay();
+    return;
+  }
   // win[j]: the input row of extended index t0 + j, where extended indices
   // 0..H-1 are the stored history and H + t is token t.
   float win[H + TT][8], w[8 * W];
@@ -477,8 +494,10 @@ __global__ __launch_bounds__(64) void conv_norm_wide_kernel(
         lo[e] = lw;
       }
       bf16_bits *dst = reinterpret_cast<bf16_bits *>(convolved) + (t0 + u) * conv_dim + c;
-      *reinterpret_cast<u32x4 *>(dst) = hi;
-      *reinterpret_cast<u32x4 *>(dst + tokens * conv_dim) = lo;
+      // Streaming stores (the planes are read by the next kernels from the
+      // MALL): 9.1 -> 7.8 us at T=512, 8192 channels.
+      __builtin_nontemporal_store(hi, reinterpret_cast<u32x4 *>(dst));
+      __builtin_nontemporal_store(lo, reinterpret_cast<u32x4 *>(dst + tokens * conv_dim));
     } else {
       float *dst = convolved + (t0 + u) * conv_dim + c;
       *reinterpret_cast<float4 *>(dst) = make_float4(y[0], y[1], y[2], y[3]);
@@ -498,16 +517,7 @@ __global__ __launch_bounds__(64) void conv_norm_wide_kernel(
 #pragma unroll
     for (int j = 0; j < 2 * H; ++j) hp[j] = make_float4(nh[4 * j], nh[4 * j + 1], nh[4 * j + 2], nh[4 * j + 3]);
   }
-  if (blockIdx.y == 0) {
-    for (int i = threadIdx.x; i < TT * static_cast<int>(hv); i += 64) {
-      const std::size_t t = t0 + i / hv, h = i % hv;
-      if (t >= tokens) break;
-      const float b = Elem<T>::load(in.b, t * in.b_stride + h);
-      const float a = Elem<T>::load(in.a, t * in.a_stride + h);
-      beta[t * hv + h] = sigmoid(b);
-      gdecay[t * hv + h] = Elem<Wt>::load(recurrent_a, h) * softplus(a + Elem<Wt>::load(dt_bias, h));
-    }
-  }
+  if (blockIdx.y == 0 && gridDim.y * static_cast<std::size_t>(kConvWideChannels) == conv_dim) beta_decay();
 }
 
 // Shifts the convolution history of the channels this thread owns (channel
@@ -2361,9 +2371,9 @@ void launch_typed(const DeltaSources &src, const void *conv_weight, const void *
           in, static_cast<const Wt *>(conv_weight), conv_state, static_cast<const Wt *>(recurrent_a),
           static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, s.tokens,
           c.conv_dim, 2 * c.key_size, s.value_heads);
-    else if (split_chunked)
+    else if (split_chunked) // (an extra row of blocks computes beta and the decay)
       conv_norm_wide_kernel<T, Wt, 4, kConvTokens, false, true>
-          <<<dim3(static_cast<unsigned>(ceil_div_unchecked(s.tokens, kConvTokens)), blocks_y, 1), 64, 0,
+          <<<dim3(static_cast<unsigned>(ceil_div_unchecked(s.tokens, kConvTokens)), blocks_y + 1, 1), 64, 0,
              stream>>>(
               in, static_cast<const Wt *>(conv_weight), conv_state, static_cast<const Wt *>(recurrent_a),
               static_cast<const Wt *>(dt_bias), convolved, beta, gdecay, s.tokens,
