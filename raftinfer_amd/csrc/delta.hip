@@ -2270,6 +2270,143 @@ __global__ __launch_bounds__(256) void out_norm_kernel(DeltaRows<T> in,
   }
 }
 
+// One-token call of the Qwen3.5 shape in one kernel: convolution, SiLU,
+// q/k L2 norm, beta / decay, recurrence and output norm.  One workgroup per
+// key head kh with two 8-wave groups, one per value head kh + g * hk (g = 0,
+// 1; hv = 2 hk), so the key head's q/k channels are convolved, and their
+// history shifted, by one workgroup only: no workgroup reads a history that
+// another one writes.  Thread cs < 512 of the workgroup owns channel slot cs
+// (q 0..127, k 128..255, v of group 0 256..383, v of group 1 384..511) and
+// shifts that channel's history itself.  The recurrence part is
+// recurrent_head_norm_kernel's, with q, k, v from LDS.
+template <typename T, typename Wt>
+__global__ __launch_bounds__(1024) void decode_step_fused_kernel(
+    DeltaRows<T> in, const Wt *__restrict__ conv_w, float *__restrict__ conv_state,
+    const Wt *__restrict__ recurrent_a, const Wt *__restrict__ dt_bias, float *__restrict__ state,
+    const Wt *__restrict__ norm_w, T *__restrict__ output, std::size_t hk, std::size_t hv,
+    float eps) {
+  constexpr int kDim = 128, kRows = 8, H = 3;
+  __shared__ float cv[4][kDim];         // normalised q, k; v of groups 0, 1
+  __shared__ float part_ss[4];          // q / k sum-of-squares halves (wave 0..3)
+  __shared__ float bd[2][2];            // [group][beta, decay]
+  __shared__ float4 red[2][2][8][32];   // [group][kv / o][wave][column quad]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int g = tid >> 9, lt = tid & 511, wave = lt >> 6;
+  const std::size_t kh = blockIdx.x;
+  const std::size_t h = kh + g * hk;
+  const std::size_t key_size = hk * kDim;
+  const int cq = lt & 31, rg = lt >> 5;
+  const int c0 = 4 * cq, r0 = kRows * rg;
+  // this group's state rows, issued before the convolution
+  float *sh = state + h * kDim * kDim;
+  float4 s[kRows];
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) s[i] = *reinterpret_cast<const float4 *>(sh + (r0 + i) * kDim + c0);
+  float nw[4], z[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    nw[i] = Elem<Wt>::load(norm_w, c0 + i);
+    z[i] = in.gate(0, h * kDim + c0 + i);
+  }
+  if (tid < 512) {
+    const int cs = tid;
+    const std::size_t ch = cs < 128   ? kh * kDim + cs
+                           : cs < 256 ? key_size + kh * kDim + (cs - 128)
+                                      : 2 * key_size + (kh + (cs >= 384 ? hk : 0)) * kDim + (cs & 127);
+    const float cur = in.x(0, ch);
+    float hist[H], w[H + 1];
+#pragma unroll
+    for (int j = 0; j < H; ++j) hist[j] = conv_state[ch * H + j];
+#pragma unroll
+    for (int j = 0; j <= H; ++j) w[j] = Elem<Wt>::load(conv_w, ch * (H + 1) + j);
+    float sum = cur * w[H];
+#pragma unroll
+    for (int j = 0; j < H; ++j) sum += hist[j] * w[j];
+    const float y = silu(sum);
+    conv_state[ch * H + 0] = hist[1];
+    conv_state[ch * H + 1] = hist[2];
+    conv_state[ch * H + 2] = cur;
+    float ss = y * y;
+    ss = sum_xor32(sum_xor16(row16_sum(ss)));
+    if (cs < 256 && lane == 0) part_ss[cs >> 6] = ss;
+    cv[cs >> 7][cs & 127] = y;
+  } else if (tid < 514) {
+    const int gg = tid - 512;
+    const std::size_t hh = kh + gg * hk;
+    const float b = Elem<T>::load(in.b, hh);
+    const float a = Elem<T>::load(in.a, hh);
+    bd[gg][0] = sigmoid(b);
+    bd[gg][1] = __expf(Elem<Wt>::load(recurrent_a, hh) * softplus(a + Elem<Wt>::load(dt_bias, hh)));
+  }
+  __syncthreads();
+  const float qn = (1.0f / sqrtf(static_cast<float>(kDim))) / sqrtf(part_ss[0] + part_ss[1] + kQkNormEpsilon);
+  const float kn = 1.0f / sqrtf(part_ss[2] + part_ss[3] + kQkNormEpsilon);
+  auto row_sum = [&](float4 x, int which) {
+    // lane ^ 32 holds the other row group of this wave for the same quad
+    x.x = sum_xor32(x.x);
+    x.y = sum_xor32(x.y);
+    x.z = sum_xor32(x.z);
+    x.w = sum_xor32(x.w);
+    if (lane < 32) red[g][which][wave][cq] = x;
+    __syncthreads();
+    float4 t = red[g][which][0][cq];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) {
+      const float4 u = red[g][which][w][cq];
+      t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+    }
+    return t;
+  };
+  const float b = bd[g][0], decay = bd[g][1];
+  float kr[kRows], qr[kRows];
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    kr[i] = cv[1][r0 + i] * kn;
+    qr[i] = cv[0][r0 + i] * qn;
+  }
+  float vv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) vv[i] = cv[2 + g][c0 + i];
+  float4 part = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    s[i].x *= decay; s[i].y *= decay; s[i].z *= decay; s[i].w *= decay;
+    part.x = fmaf(s[i].x, kr[i], part.x);
+    part.y = fmaf(s[i].y, kr[i], part.y);
+    part.z = fmaf(s[i].z, kr[i], part.z);
+    part.w = fmaf(s[i].w, kr[i], part.w);
+  }
+  const float4 kv = row_sum(part, 0);
+  const float4 d = make_float4((vv[0] - kv.x) * b, (vv[1] - kv.y) * b, (vv[2] - kv.z) * b, (vv[3] - kv.w) * b);
+  float4 po = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    s[i].x = fmaf(kr[i], d.x, s[i].x);
+    s[i].y = fmaf(kr[i], d.y, s[i].y);
+    s[i].z = fmaf(kr[i], d.z, s[i].z);
+    s[i].w = fmaf(kr[i], d.w, s[i].w);
+    po.x = fmaf(s[i].x, qr[i], po.x);
+    po.y = fmaf(s[i].y, qr[i], po.y);
+    po.z = fmaf(s[i].z, qr[i], po.z);
+    po.w = fmaf(s[i].w, qr[i], po.w);
+  }
+  const float4 o = row_sum(po, 1);
+  if (wave == 0) {
+    // lanes 0..31 cover the 32 column quads (lanes 32..63 repeat them)
+    float ss = o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w;
+    ss = sum_xor16(row16_sum(ss));
+    const float scale = rsqrtf(ss / static_cast<float>(kDim) + eps);
+    if (lane < 32) {
+      const std::size_t base = h * kDim + c0;
+      const float ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Elem<T>::store(output, base + i, ov[i] * scale * nw[i] * silu(z[i]));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) *reinterpret_cast<float4 *>(sh + (r0 + i) * kDim + c0) = s[i];
+}
+
 // ------------------------------------------------------------ launchers
 
 template <typename InT, typename OutT>
@@ -2364,6 +2501,17 @@ void launch_typed(const DeltaSources &src, const void *conv_weight, const void *
   const bool split_chunked = wide && chunked && !one_token_state && s.key_dim == kChunkDim &&
                              s.value_dim == kChunkDim;
   constexpr int kConvTokens = 4; // tokens per workgroup of the multi-token convolution
+  // A one-token call of the model shape (two value heads per key head): the
+  // convolution, recurrence and output norm in one kernel.
+  if (one_token_state && s.value_heads == 2 * s.key_heads && !chunked &&
+      (reinterpret_cast<std::uintptr_t>(rec_state) & 15u) == 0) {
+    decode_step_fused_kernel<T, Wt><<<static_cast<unsigned>(s.key_heads), 1024, 0, stream>>>(
+        in, static_cast<const Wt *>(conv_weight), conv_state, static_cast<const Wt *>(recurrent_a),
+        static_cast<const Wt *>(dt_bias), rec_state, static_cast<const Wt *>(norm_w), static_cast<T *>(output),
+        s.key_heads, s.value_heads, s.epsilon);
+    check_launch<Err>("qwen35_gated_delta fused decode step");
+    return;
+  }
   if (wide) {
     const unsigned blocks_y = static_cast<unsigned>(c.conv_dim / kConvWideChannels);
     if (one_token_state)
