@@ -2297,11 +2297,16 @@ __global__ __launch_bounds__(1024) void decode_step_fused_kernel(
   const std::size_t key_size = hk * kDim;
   const int cq = lt & 31, rg = lt >> 5;
   const int c0 = 4 * cq, r0 = kRows * rg;
-  // this group's state rows, issued before the convolution
+  // This group's state rows go to LDS by LDS-direct loads (the CU fetches
+  // about twice as fast that way as into registers), issued before anything
+  // else; each thread reads its own 8 rows x 16 bytes back after the
+  // convolution.  Instruction i of a wave moves row r0 + i of both row groups
+  // of the wave (lanes 0-31, 32-63).
+  __shared__ float4 stage[16][kRows][64];
   float *sh = state + h * kDim * kDim;
-  float4 s[kRows];
 #pragma unroll
-  for (int i = 0; i < kRows; ++i) s[i] = *reinterpret_cast<const float4 *>(sh + (r0 + i) * kDim + c0);
+  for (int i = 0; i < kRows; ++i)
+    load_lds_b128(sh, static_cast<std::uint32_t>(((r0 + i) * kDim + c0) * 4), lds_address(&stage[tid >> 6][i][0]));
   float nw[4], z[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -2358,6 +2363,10 @@ __global__ __launch_bounds__(1024) void decode_step_fused_kernel(
     return t;
   };
   const float b = bd[g][0], decay = bd[g][1];
+  wait_vm<0>(); // this thread's state rows have landed (the barrier above waited for every wave's)
+  float4 s[kRows];
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) s[i] = stage[tid >> 6][i][lane];
   float kr[kRows], qr[kRows];
 #pragma unroll
   for (int i = 0; i < kRows; ++i) {
