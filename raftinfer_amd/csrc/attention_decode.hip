@@ -731,8 +731,13 @@ void launch_decode_mfma(const DecodeMfmaArgs &args, const bf16_bits *g, std::siz
     // Above two chunks per wave the LDS-staged scan streams the next chunk
     // under the current one (ctx 1024: 11.2 -> 10.3 us hot); at ctx <= 512
     // the register-fed scan is as fast or faster cold.
+    // (The stage's LDS-direct loads of the new row need 16-byte aligned
+    // key / value rows; other pointers take the register-fed scan.)
     const std::size_t ctx_bound = dynamic ? shape.max_context_tokens : host_ctx;
-    if (ctx_bound > 2 * kSingleMfmaWaves * 32)
+    const bool rows_aligned =
+        ((reinterpret_cast<std::uintptr_t>(args.key_new) | reinterpret_cast<std::uintptr_t>(args.value_new)) &
+         15u) == 0;
+    if (ctx_bound > 2 * kSingleMfmaWaves * 32 && rows_aligned)
       decode_single_mfma_kernel<kSingleDs, kSingleMfmaWaves, kFused, true>
           <<<xcd_grid<kSingleDs>(kKvHeads), kSingleMfmaWaves * 64, 0, stream>>>(
               args, g, gate_stride, out, shape.past_tokens, device_position,
