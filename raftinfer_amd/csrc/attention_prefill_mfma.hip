@@ -175,7 +175,6 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
   const int col_tok = col & (kQTok - 1);
   const std::size_t col_row = static_cast<std::size_t>(col_tok) < q_rows ? col_tok : q_rows - 1;
   const std::size_t col_pos = past + t0 + col_row;
-  const std::size_t col_head = kv_head * kGroup + (col >> 3);
   const int wave_u = __builtin_amdgcn_readfirstlane(wave); // wave index as a scalar
   // Element offset of column c's row (head c / 8, token c % 8, clamped to the
   // tile's tokens) in the query / gate / output layout [T][16][256].

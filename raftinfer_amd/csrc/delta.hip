@@ -1274,10 +1274,6 @@ struct Scan3Shared {
 __device__ __forceinline__ int swz128(int r, int c) { return r * kChunkDim + ((c ^ (r & 15)) << 3); }
 __device__ __forceinline__ int swz64(int r, int c) { return r * kChunk + ((c ^ ((r >> 1) & 7)) << 3); }
 
-__device__ __forceinline__ floatx4 mfma_bf16(const bf16_bits *a, const bf16_bits *b, floatx4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(lds8(a), lds8(b), c, 0, 0, 0);
-}
-
 // LDS-direct load of rows row0 .. row0+ROWS-1 of halves 0 .. HALVES-1 of a
 // bf16 [2][R][C] record block at byte offset `off` into its swizzled LDS copy
 // `dst` (same shape).  One instruction moves 1 KiB = 1024 / (2 C) rows; lane
@@ -1431,7 +1427,6 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkScratch scratch,
       floatx4 dv, fv;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int i = i0 + 4 * lk + r;
         dv[r] = u[r] - acc[r];
         fv[r] = fdec[r] * dv[r];
       }
@@ -2283,8 +2278,7 @@ template <typename T, typename Wt>
 __global__ __launch_bounds__(1024) void decode_step_fused_kernel(
     DeltaRows<T> in, const Wt *__restrict__ conv_w, float *__restrict__ conv_state,
     const Wt *__restrict__ recurrent_a, const Wt *__restrict__ dt_bias, float *__restrict__ state,
-    const Wt *__restrict__ norm_w, T *__restrict__ output, std::size_t hk, std::size_t hv,
-    float eps) {
+    const Wt *__restrict__ norm_w, T *__restrict__ output, std::size_t hk, float eps) {
   constexpr int kDim = 128, kRows = 8, H = 3;
   __shared__ float cv[4][kDim];         // normalised q, k; v of groups 0, 1
   __shared__ float part_ss[4];          // q / k sum-of-squares halves (wave 0..3)
@@ -2517,7 +2511,7 @@ void launch_typed(const DeltaSources &src, const void *conv_weight, const void *
     decode_step_fused_kernel<T, Wt><<<static_cast<unsigned>(s.key_heads), 1024, 0, stream>>>(
         in, static_cast<const Wt *>(conv_weight), conv_state, static_cast<const Wt *>(recurrent_a),
         static_cast<const Wt *>(dt_bias), rec_state, static_cast<const Wt *>(norm_w), static_cast<T *>(output),
-        s.key_heads, s.value_heads, s.epsilon);
+        s.key_heads, s.epsilon);
     check_launch<Err>("qwen35_gated_delta fused decode step");
     return;
   }
