@@ -14,8 +14,7 @@
 //               instruction, no VGPRs); the next tile's K is issued as soon as
 //               the current K tile has been read, its V after the current V
 //               tile.  Rows are stored as 32 16-byte chunks with chunk c at
-//               c ^ swz(row), so both operand reads below are free of bank
-//               conflicts;
+//               c ^ swz(row) (see swz for the bank conflicts this leaves);
 //   S^T = K Q^T 16 x v_mfma_f32_32x32x16_bf16, K and Q rows read from LDS
 //               with ds_read_b128 four MFMAs ahead (the Q tile is staged once
 //               per workgroup, in the K tile's chunk order);
@@ -81,9 +80,13 @@ struct NormQShared {
   float rot[kQTok][kHeadDim];    // per token slot: cos[pairs] then sin[pairs]
 };
 
-// Physical 16-byte chunk of logical chunk c in tile row r: c ^ (r & 7).  An
-// 8-lane group of a ds_read_b128 (8 rows, one logical chunk) and a 16-lane
-// group of a ds_read_b64_tr_b16 (4 rows x 4 chunks) then hit distinct banks.
+// Physical 16-byte chunk of logical chunk c in tile row r: c ^ (r & 7).  The
+// LDS bank-conflict counter, calibrated on these access patterns alone, shows
+// this leaves 2-way conflicts on the K/Q ds_read_b128 (16 rows per pass) and
+// 4-way on the V ds_read_b64_tr_b16; c ^ (4 (r % 4) + (r / 4) % 4) is free of
+// both, but measured PP512 13.2 -> 13.1 us, PP2048 80 -> 78, PP128 7.13 ->
+// 7.3 (more lane bases held across the loop), so the loop is not bound by
+// these reads and the simpler swizzle stays.
 __device__ __forceinline__ int swz(int r) { return r & 7; }
 
 __device__ __forceinline__ int chunk_offset(int r, int c) { // in bf16 elements
