@@ -210,6 +210,31 @@ def test_core_chunked_ragged_lengths_with_state(gpu, T):
     assert_bf16_close(got_o, bf16(want_o), what=f"chunked core T={T}")
 
 
+def test_core_chunked_long_prompt(gpu):
+    """T=2048 (32 chunks): the state carried through a long scan stays within
+    rel-L2 1e-4 of the token recurrence, and every output row within the bf16 gate."""
+    T = 2048
+    q, k, v, beta, g = cfg5_inputs(T, 4242)
+    s0 = normal(rng(4243), 32, 128, 128, scale=0.05)
+    want_o, want_s = orc.delta_core(q, k, v, beta, g, 1 / np.sqrt(128), s0)
+    got_o, got_s = run_core(q, k, v, beta, g, s0, chunked=True)
+    assert rel_l2(got_s, want_s) < 1e-4
+    assert_bf16_close(got_o, bf16(want_o), what="chunked core T=2048")
+
+
+def test_full_entry_long_prompt(gpu):
+    # The drop-in entry at T=1024 (16 chunks through the split-plane path) from non-zero states.
+    sh = model_shape(1024)
+    fx = fixture_for(sh, seed=1024)
+    r = rng(1025)
+    rec0 = normal(r, 32 * 128 * 128, scale=0.05)
+    conv0 = normal(r, 8192 * 3)
+    got = run_gpu(sh, fx, 3, 3, conv0, rec0)
+    want = run_ref(sh, fx, 3, 3, conv0, rec0)
+    check(got, want)
+    assert rel_l2(got[2], want[2]) < 1e-4
+
+
 @pytest.mark.parametrize("hk,hv", [(8, 32), (32, 32), (4, 8)])
 def test_core_chunked_head_groupings(gpu, hk, hv):
     """Value head h reads key head h % Hk; the chunk kernels index K and Q
