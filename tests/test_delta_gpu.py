@@ -261,6 +261,26 @@ def test_core_chunked_head_groupings(gpu, hk, hv):
     assert_bf16_close(from_dev(out), bf16(want_o), what=f"chunked core hk={hk} hv={hv}")
 
 
+@pytest.mark.parametrize("hk,hv", [(8, 16), (16, 16), (8, 32)])
+@pytest.mark.parametrize("T", [1, 130])
+def test_full_entry_head_groupings(gpu, hk, hv, T):
+    """The full entry on head counts other than 16 / 32 whose widths still take
+    the channel-spread convolution: (8, 16) the fused one-token step with 8
+    workgroups, (16, 16) and (8, 32) key groups of 1 and 4 (the recurrent and
+    chunked kernels behind the wide convolution), from non-zero states."""
+    sh = dict(tokens=T, hidden=hv * 128, hk=hk, hv=hv, dk=128, dv=128, width=4, eps=1e-6)
+    cd = 2 * hk * 128 + hv * 128
+    fx = fixture_for(sh, seed=700 + hk + hv + T)
+    r = rng(701 + hk + hv + T)
+    rec0 = normal(r, hv * 128 * 128, scale=0.05)
+    conv0 = normal(r, cd * 3)
+    got = run_gpu(sh, fx, 3, 3, conv0, rec0)
+    want = run_ref(sh, fx, 3, 3, conv0, rec0)
+    check(got, want)
+    assert rel_l2(got[2], want[2]) < 1e-4
+    assert np.array_equal(got[1], want[1]) or rel_l2(got[1], want[1]) < 1e-6
+
+
 def test_core_chunked_equals_recurrent(gpu):
     T = 200
     q, k, v, beta, g = cfg5_inputs(T, 7)
