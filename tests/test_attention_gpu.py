@@ -180,6 +180,18 @@ def test_single_block_staged_scan(gpu, layout, ctx):
         assert np.array_equal(ck, keys) and np.array_equal(cv, vals)
 
 
+@pytest.mark.parametrize("ctx", [1, 2, 31, 33, 100, 300])
+def test_single_block_staged_scan_short_context(gpu, ctx):
+    # A device position with max_ctx above 512 selects the staged scan whatever
+    # the position, so short contexts (waves with no chunk, one ragged chunk)
+    # run through it too.
+    out, expect, cache, keys, vals, _, _ = run_decode(3, 1, 1, ctx, 2048, mode=1, device_position=True,
+                                                      seed=ctx + 4000, heavy_rows=0.01)
+    assert_bf16_close(out, bf16(expect), what=f"staged single-block ctx {ctx}")
+    ck, cv = read_cache(cache, 1, ctx, 2048)
+    assert np.array_equal(ck, keys) and np.array_equal(cv, vals)
+
+
 def test_single_block_equals_split(gpu):
     a, *_ = run_decode(3, 1, 1, 1500, 2048, mode=1, seed=99)
     b, *_ = run_decode(3, 1, 1, 1500, 2048, mode=2, seed=99)
