@@ -75,7 +75,7 @@ struct PrefillNormRope {
   double ratio; // rope_base^(-2 / rotary_dim)
   float epsilon;
 };
-struct NormQShared {
+struct alignas(16) NormQShared {
   float weight[kHeadDim];        // the staged norm weight (bf16 uses the first half)
   float rot[kQTok][kHeadDim];    // per token slot: cos[pairs] then sin[pairs]
 };
@@ -130,6 +130,133 @@ __device__ __forceinline__ void scale_agpr(floatx16 &o, float s) {
 __device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory"); }
 
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// The q producer's RMSNorm + RoPE (norm_rope_256_lane) applied in place to
+// the staged Q rows, bit for bit.
+//
+// Sliced form (rotary pairs a multiple of 32): eight lanes per row, lane g of
+// the row owning dims 32g .. 32g+31, so a wave finishes its 8 rows at once
+// with one LDS round trip.  The sum of squares is formed as the same tree the
+// lane-wise form builds across 64 lanes: per 4 dims an fma chain, then
+// pairwise sums of neighbouring 4-dim partials in lane order (levels 1-3 in
+// the lane, levels 4-6 by DPP over the row's 8 lanes); every level adds the
+// same two operands, so the result is bit-identical.  The RoPE partner of dim
+// d sits in lane g +- pairs / 32 at the same offset.
+__device__ __forceinline__ void norm_rope_rows_sliced(bf16_bits *q, int r, int g, const float *weight,
+                                                      bool weight_f32, int pairs, const float *rot,
+                                                      float epsilon) {
+  bf16_bits *row = q + r * kHeadDim;
+  u32x4 raw[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) raw[j] = *reinterpret_cast<const u32x4 *>(row + (((4 * g + j) ^ swz(r)) << 3));
+  float x[32];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[8 * j + 2 * e] = bf16_lo(raw[j][e]);
+      x[8 * j + 2 * e + 1] = bf16_hi(raw[j][e]);
+    }
+  float pp[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s = fmaf(x[4 * k + e], x[4 * k + e], s);
+    pp[k] = s;
+  }
+  float ss = ((pp[0] + pp[1]) + (pp[2] + pp[3])) + ((pp[4] + pp[5]) + (pp[6] + pp[7]));
+  ss += dpp<kDppXor1>(ss);
+  ss += dpp<kDppXor2>(ss);
+  ss += dpp<kDppHalfMirror>(ss);
+  const float scale = 1.0f / sqrtf(ss * (1.0f / 256.0f) + epsilon);
+  float w[32];
+  if (weight_f32) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float4 t = reinterpret_cast<const float4 *>(weight)[8 * g + k];
+      w[4 * k] = t.x; w[4 * k + 1] = t.y; w[4 * k + 2] = t.z; w[4 * k + 3] = t.w;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const u32x4 t = reinterpret_cast<const u32x4 *>(weight)[4 * g + k];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        w[8 * k + 2 * e] = bf16_lo(t[e]);
+        w[8 * k + 2 * e + 1] = bf16_hi(t[e]);
+      }
+    }
+  }
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) v[i] = x[i] * scale * w[i];
+  const int pg = pairs / 32; // lane groups between a dim and its partner
+  const bool rotated = g < 2 * pg, first = g < pg;
+  // Partner lane: g xor 1 (pg = 1) or g xor 2 (pg = 2) among the row's
+  // lanes, by DPP; other widths through the LDS crossbar.
+  float pv[32];
+  if (pg == 1) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) pv[i] = dpp<kDppXor1>(v[i]);
+  } else if (pg == 2) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) pv[i] = dpp<kDppXor2>(v[i]);
+  } else {
+    const int lane = threadIdx.x & 63;
+    const int src_lane = first ? lane + pg : lane - pg;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) pv[i] = __shfl(v[i], src_lane);
+  }
+  if (rotated) {
+    // cos and sin of pairs p0 .. p0+31: 16-byte aligned (pairs and p0 are
+    // multiples of 32), read as 16 vectors before any is used.
+    const int p0 = 32 * (first ? g : g - pg);
+    float4 cs4[8], sn4[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      cs4[k] = reinterpret_cast<const float4 *>(rot + p0)[k];
+      sn4[k] = reinterpret_cast<const float4 *>(rot + pairs + p0)[k];
+    }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const float4 &c4 = cs4[i >> 2], &s4 = sn4[i >> 2];
+      const float c = (i & 3) == 0 ? c4.x : (i & 3) == 1 ? c4.y : (i & 3) == 2 ? c4.z : c4.w;
+      const float sn = (i & 3) == 0 ? s4.x : (i & 3) == 1 ? s4.y : (i & 3) == 2 ? s4.z : s4.w;
+      v[i] = first ? v[i] * c - pv[i] * sn : pv[i] * sn + v[i] * c;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    *reinterpret_cast<u32x4 *>(row + (((4 * g + j) ^ swz(r)) << 3)) =
+        u32x4{pack_bf16x2(v[8 * j], v[8 * j + 1]), pack_bf16x2(v[8 * j + 2], v[8 * j + 3]),
+              pack_bf16x2(v[8 * j + 4], v[8 * j + 5]), pack_bf16x2(v[8 * j + 6], v[8 * j + 7])};
+}
+
+// Lane-wise form (any rotary width): rows 8w .. 8w+7 one at a time, lane l
+// owning dims 4l .. 4l+3 (8 bytes of logical chunk l / 2).
+__device__ __forceinline__ void norm_rope_rows_lanewise(bf16_bits *q, int wave, int lane, const float *weight,
+                                                        bool weight_f32, int pairs, const float (*rot)[kHeadDim],
+                                                        float epsilon) {
+  float w[4];
+  if (weight_f32) {
+    const float4 x = reinterpret_cast<const float4 *>(weight)[lane];
+    w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
+  } else {
+    const u32x2 x = reinterpret_cast<const u32x2 *>(weight)[lane];
+    w[0] = bf16_lo(x[0]); w[1] = bf16_hi(x[0]); w[2] = bf16_lo(x[1]); w[3] = bf16_hi(x[1]);
+  }
+#pragma unroll
+  for (int rr = 0; rr < 8; ++rr) {
+    const int r = 8 * wave + rr;
+    u32x2 *slot = reinterpret_cast<u32x2 *>(q + chunk_offset(r, lane >> 1) + 4 * (lane & 1));
+    const u32x2 raw = *slot;
+    const float x[4] = {bf16_lo(raw[0]), bf16_hi(raw[0]), bf16_lo(raw[1]), bf16_hi(raw[1])};
+    float v[4];
+    norm_rope_256_lane(x, w, lane, pairs, rot[r & (kQTok - 1)], epsilon, v);
+    *slot = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  }
+}
 
 // FromInput: past == 0 and every key is read from the key/value inputs
 // ([tokens][4][256]); the workgroup also writes its own tokens' rows into the
@@ -322,26 +449,11 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
   if (t < n_tiles) wait_vm<32 + kLateLoads>(); else wait_vm<0>(); // this wave's Q rows have landed
   __syncthreads(); // ... and every other wave's
   if constexpr (NormQ) {
-    // RMSNorm + RoPE of rows 8w .. 8w+7 in place: lane l owns dims 4l .. 4l+3
-    // (8 bytes of logical chunk l / 2); bf16 results as the producer stores them.
-    float w[4];
-    if (nq.weight_f32) {
-      const float4 x = reinterpret_cast<const float4 *>(nqs->weight)[lane];
-      w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
-    } else {
-      const u32x2 x = reinterpret_cast<const u32x2 *>(nqs->weight)[lane];
-      w[0] = bf16_lo(x[0]); w[1] = bf16_hi(x[0]); w[2] = bf16_lo(x[1]); w[3] = bf16_hi(x[1]);
-    }
-#pragma unroll
-    for (int rr = 0; rr < 8; ++rr) {
-      const int r = 8 * wave_u + rr;
-      u32x2 *slot = reinterpret_cast<u32x2 *>(sh.q + chunk_offset(r, lane >> 1) + 4 * (lane & 1));
-      const u32x2 raw = *slot;
-      const float x[4] = {bf16_lo(raw[0]), bf16_hi(raw[0]), bf16_lo(raw[1]), bf16_hi(raw[1])};
-      float v[4];
-      norm_rope_256_lane(x, w, lane, nq.pairs, nqs->rot[r & (kQTok - 1)], nq.epsilon, v);
-      *slot = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-    }
+    if (nq.pairs % 32 == 0)
+      norm_rope_rows_sliced(sh.q, 8 * wave_u + (lane >> 3), lane & 7, nqs->weight, nq.weight_f32, nq.pairs,
+                            nqs->rot[(lane >> 3) & (kQTok - 1)], nq.epsilon);
+    else
+      norm_rope_rows_lanewise(sh.q, wave_u, lane, nqs->weight, nq.weight_f32, nq.pairs, nqs->rot, nq.epsilon);
     __syncthreads(); // every row is normalised
   }
   for (; t < n_tiles; t += kWaves) {

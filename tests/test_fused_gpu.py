@@ -145,7 +145,8 @@ def test_fused_prefill_equals_producers_then_attention(gpu, T, past):
 
 @pytest.mark.parametrize("rot,wdt,layout", [(256, torch.float32, ops.HEAD_MAJOR),
                                             (8, torch.bfloat16, ops.TOKEN_MAJOR),
-                                            (128, torch.float32, ops.TOKEN_MAJOR)])
+                                            (128, torch.float32, ops.TOKEN_MAJOR),
+                                            (192, torch.bfloat16, ops.HEAD_MAJOR)])
 def test_fused_prefill_rotary_weights_layouts(gpu, rot, wdt, layout):
     c = _prefill_case(70, 5, rot, wdt, layout, seed=rot + 1)
     assert torch.equal(c["cache1"], c["cache2"])
