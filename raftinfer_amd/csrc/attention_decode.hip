@@ -428,38 +428,64 @@ struct FusedNormRope {
 // RMSNorm + RoPE of the group's four q heads and of its key row at
 // `position`, into LDS (waves 0..3: q heads, wave 4: k; the workgroup has at
 // least 5 waves), with exactly the arithmetic of the producer kernels.
-__device__ __forceinline__ void fused_qk_prologue(const FusedNormRope &f, std::size_t kv_head,
-                                                  std::size_t position, DecodeFusedQK &fq) {
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  float x[4] = {0.f, 0.f, 0.f, 0.f}, w[4] = {0.f, 0.f, 0.f, 0.f};
-  if (wave <= kGroup) {
-    const bf16_bits *src = wave < kGroup ? f.query_gate + (kv_head * kGroup + wave) * 2 * kHeadDim
-                                         : f.key + kv_head * kHeadDim;
-    const u32x2 r = *reinterpret_cast<const u32x2 *>(src + 4 * lane);
-    x[0] = bf16_lo(r[0]); x[1] = bf16_hi(r[0]); x[2] = bf16_lo(r[1]); x[3] = bf16_hi(r[1]);
-    const void *wp = wave < kGroup ? f.q_weight : f.k_weight;
-    if (f.weight_f32) {
-      const float4 ww = reinterpret_cast<const float4 *>(wp)[lane];
-      w[0] = ww.x; w[1] = ww.y; w[2] = ww.z; w[3] = ww.w;
-    } else {
-      const u32x2 ww = reinterpret_cast<const u32x2 *>(wp)[lane];
-      w[0] = bf16_lo(ww[0]); w[1] = bf16_hi(ww[0]); w[2] = bf16_lo(ww[1]); w[3] = bf16_hi(ww[1]);
-    }
-  }
+// Its loads and its arithmetic are split so that a caller can issue other
+// loads in between (fused_qk_load, then fused_qk_finish).
+struct FusedQKRows { // raw bits: converting them at the load would wait for it there
+  u32x2 x;
+  u32x2 w0, w1; // f32 weights (w0, w1), or bf16 weights (w0; w1 re-reads them)
+};
+__device__ __forceinline__ FusedQKRows fused_qk_load(const FusedNormRope &f, std::size_t kv_head) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // Waves past the group read the first row; their values are not used.
+  const int row = wave <= kGroup ? wave : 0;
+  const bf16_bits *src = row < kGroup ? f.query_gate + (kv_head * kGroup + row) * 2 * kHeadDim
+                                      : f.key + kv_head * kHeadDim;
+  const auto *wp = static_cast<const unsigned char *>(row < kGroup ? f.q_weight : f.k_weight);
+  // Unconditional loads (the address, not the load, depends on the weight
+  // type), so no value is merged across branches.
+  const std::size_t w0 = f.weight_f32 ? 16u * lane : 8u * lane;
+  const std::size_t w1 = f.weight_f32 ? 16u * lane + 8u : 8u * lane;
+  return FusedQKRows{*reinterpret_cast<const u32x2 *>(src + 4 * lane), *reinterpret_cast<const u32x2 *>(wp + w0),
+                     *reinterpret_cast<const u32x2 *>(wp + w1)};
+}
+// The rotation table of `position` (read after the next barrier).  It runs
+// before the loads are issued: with the loaded raw values live across its
+// per-lane branches, the compiler reused one of their registers inside them.
+__device__ __forceinline__ void fused_qk_rot(const FusedNormRope &f, std::size_t position, DecodeFusedQK &fq) {
+  const int tid = threadIdx.x;
   if (tid < f.pairs) {
     float cs, sn;
     rope_cos_sin(tid, position, f.ratio, cs, sn);
     fq.rot[tid] = cs;
     fq.rot[f.pairs + tid] = sn;
   }
+}
+__device__ __forceinline__ void fused_qk_finish(const FusedNormRope &f, const FusedQKRows &r, DecodeFusedQK &fq) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   __syncthreads();
   if (wave <= kGroup) {
+    const float x[4] = {bf16_lo(r.x[0]), bf16_hi(r.x[0]), bf16_lo(r.x[1]), bf16_hi(r.x[1])};
+    float w[4];
+    if (f.weight_f32) {
+      // (Element by element through a scalar: this compiler's
+      // __builtin_bit_cast of a vector element reads element 0.)
+      const std::uint32_t b[4] = {r.w0[0], r.w0[1], r.w1[0], r.w1[1]};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = __builtin_bit_cast(float, b[e]);
+    } else {
+      w[0] = bf16_lo(r.w0[0]); w[1] = bf16_hi(r.w0[0]); w[2] = bf16_lo(r.w0[1]); w[3] = bf16_hi(r.w0[1]);
+    }
     float v[4];
     norm_rope_256_lane(x, w, lane, f.pairs, fq.rot, f.epsilon, v);
     bf16_bits *dst = wave < kGroup ? fq.q[wave] : fq.k;
     *reinterpret_cast<u32x2 *>(dst + 4 * lane) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
   }
   __syncthreads();
+}
+__device__ __forceinline__ void fused_qk_prologue(const FusedNormRope &f, std::size_t kv_head,
+                                                  std::size_t position, DecodeFusedQK &fq) {
+  fused_qk_rot(f, position, fq);
+  fused_qk_finish(f, fused_qk_load(f, kv_head), fq);
 }
 
 // The fused form of append_rows: the key row comes from LDS (normalised and
@@ -576,8 +602,18 @@ __device__ __forceinline__ void split_body(unsigned block, const DecodeMfmaArgs 
   const std::size_t begin = partition * partition_tokens;
   if (begin >= ctx) return;
   const std::size_t end = ctx < begin + partition_tokens ? ctx : begin + partition_tokens;
-  if constexpr (kFused) fused_qk_prologue(f, kv_head, position, fq);
-  decode_mfma_scan<DS, WAVES, CT, kFused>(a, kv_head, dq, begin, end, position, sh, &fq);
+  if constexpr (kFused) {
+    // The q / k rows are loaded first; the prologue's arithmetic runs inside
+    // the scan, once the first chunk's loads have gone out behind them.
+    fused_qk_rot(f, position, fq);
+    const FusedQKRows rows = fused_qk_load(f, kv_head);
+    __builtin_amdgcn_sched_barrier(0);
+    auto pro = [&] { fused_qk_finish(f, rows, fq); };
+    decode_mfma_scan<DS, WAVES, CT, true, false, decltype(pro)>(a, kv_head, dq, begin, end, position, sh, &fq,
+                                                                nullptr, pro);
+  } else {
+    decode_mfma_scan<DS, WAVES, CT, false>(a, kv_head, dq, begin, end, position, sh, &fq);
+  }
   __syncthreads();
   // The workgroup whose range holds the position appends the new row.  When a
   // device position lies beyond the plan's capacity no workgroup holds it (the

@@ -19,6 +19,8 @@
 
 #include "decode_scan.hpp"
 
+#include <type_traits>
+
 namespace raftinfer::amd {
 
 struct DecodeMfmaArgs {
@@ -114,12 +116,24 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 //
 // kFused: q comes from fq->q and the new token's key row from fq->k (both in
 // LDS) instead of a.query and a.key_new.
-template <int DS, int WAVES, int CT = 32, bool kFused = false, bool kDma = false>
+struct NoPrologue {
+  __device__ void operator()() const {}
+};
+
+// pro (kFused, register-fed scan only): the workgroup's q / k prologue, which
+// fills fq and holds workgroup barriers.  Each wave runs it once, right after
+// issuing its first chunk's loads (a wave without a chunk right away), so the
+// cache rows stream in while q and k are normalised; q is read from fq only
+// after it.
+template <int DS, int WAVES, int CT = 32, bool kFused = false, bool kDma = false, typename Pro = NoPrologue>
 __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::size_t kv_head,
                                                  int dq, std::size_t begin, std::size_t end,
                                                  std::size_t pos, DecodeMfmaShared<DS, WAVES, CT> &sh,
                                                  const DecodeFusedQK *fq = nullptr,
-                                                 DecodeStage<DS, WAVES, CT> *stage = nullptr) {
+                                                 DecodeStage<DS, WAVES, CT> *stage = nullptr,
+                                                 Pro pro = Pro{}) {
+  constexpr bool kPro = !std::is_same_v<Pro, NoPrologue>;
+  static_assert(!kPro || (kFused && !kDma), "the overlapped prologue is for the fused register-fed scan");
   constexpr int DIMS = kHeadDim / DS;
   constexpr int G = CT / 8; // 8-token groups per chunk
   // K is read non-temporally when at most 4 sibling workgroups share it
@@ -194,6 +208,7 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
 
   // B operand per line: column n < 8 = (half' = n/4, head n%4).
   bf16x8 qb[4];
+  auto make_qb = [&] {
 #pragma unroll
   for (int line = 0; line < 4; ++line) {
     u32x4 w = u32x4{0u, 0u, 0u, 0u};
@@ -208,6 +223,9 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
     }
     qb[line] = __builtin_bit_cast(bf16x8, w);
   }
+  };
+  bool pro_done = false;
+  if constexpr (!kPro) make_qb();
 
   float m_run = -INFINITY; // for head n (head lanes)
   float l_run = 0.f;       // per-lane partial sum for head n
@@ -283,6 +301,22 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
           kr[g][line] = kNtKeys ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(row + line * 64 + seg * 8))
                                 : *reinterpret_cast<const u32x4 *>(row + line * 64 + seg * 8);
       }
+      if constexpr (kPro) {
+        // V loads go out with K, then the prologue runs under them.
+#pragma unroll
+        for (int j = 0; j < TPL; ++j) {
+          std::size_t tok = c0 + tl + TL * j;
+          tok = tok < end ? tok : end - 1;
+          const bf16_bits *row = tok == pos ? a.value_new + kv_head * kHeadDim
+                                            : vplane + cache_row(a.head_major, tok, kv_head, a.max_ctx);
+          vv[j].load(row + dq * DIMS + VEC * dl);
+        }
+        if (!pro_done) {
+          pro();
+          make_qb();
+          pro_done = true;
+        }
+      }
       if constexpr (kFused) {
         if (pos >= c0 && pos < c0 + CT) { // this chunk holds the new token (wave-uniform)
 #pragma unroll
@@ -295,13 +329,15 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
           }
         }
       }
+      if constexpr (!kPro) {
 #pragma unroll
-      for (int j = 0; j < TPL; ++j) {
-        std::size_t tok = c0 + tl + TL * j;
-        tok = tok < end ? tok : end - 1;
-        const bf16_bits *row = tok == pos ? a.value_new + kv_head * kHeadDim
-                                          : vplane + cache_row(a.head_major, tok, kv_head, a.max_ctx);
-        vv[j].load(row + dq * DIMS + VEC * dl);
+        for (int j = 0; j < TPL; ++j) {
+          std::size_t tok = c0 + tl + TL * j;
+          tok = tok < end ? tok : end - 1;
+          const bf16_bits *row = tok == pos ? a.value_new + kv_head * kHeadDim
+                                            : vplane + cache_row(a.head_major, tok, kv_head, a.max_ctx);
+          vv[j].load(row + dq * DIMS + VEC * dl);
+        }
       }
     }
     // Keep every load of the chunk ahead of the first wait: the scheduler
@@ -362,6 +398,9 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
       }
     }
     wave_lds_order();
+  }
+  if constexpr (kPro) {
+    if (!pro_done) pro(); // a wave without a chunk
   }
   // l: the lanes of head n are n, n+16, n+32, n+48.
   const float l_tot = sum_xor32(sum_xor16(l_run));
