@@ -131,17 +131,10 @@ __device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\
 
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// The q producer's RMSNorm + RoPE (norm_rope_256_lane) applied in place to
-// the staged Q rows, bit for bit.
-//
-// Sliced form (rotary pairs a multiple of 32): eight lanes per row, lane g of
-// the row owning dims 32g .. 32g+31, so a wave finishes its 8 rows at once
-// with one LDS round trip.  The sum of squares is formed as the same tree the
-// lane-wise form builds across 64 lanes: per 4 dims an fma chain, then
-// pairwise sums of neighbouring 4-dim partials in lane order (levels 1-3 in
-// the lane, levels 4-6 by DPP over the row's 8 lanes); every level adds the
-// same two operands, so the result is bit-identical.  The RoPE partner of dim
-// d sits in lane g +- pairs / 32 at the same offset.
+// The q producer's RMSNorm + RoPE applied in place to the staged Q rows, bit
+// for bit.  Sliced form (rotary pairs a multiple of 32; norm_rope_256_slice):
+// eight lanes per row, so a wave finishes its 8 rows at once with one LDS
+// round trip.
 __device__ __forceinline__ void norm_rope_rows_sliced(bf16_bits *q, int r, int g, const float *weight,
                                                       bool weight_f32, int pairs, const float *rot,
                                                       float epsilon) {
@@ -149,88 +142,14 @@ __device__ __forceinline__ void norm_rope_rows_sliced(bf16_bits *q, int r, int g
   u32x4 raw[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) raw[j] = *reinterpret_cast<const u32x4 *>(row + (((4 * g + j) ^ swz(r)) << 3));
-  float x[32];
+  float x[32], w[32], v[32];
+  unpack_bf16x32(raw, x);
+  load_slice_weights(weight, weight_f32, g, w);
+  norm_rope_256_slice(x, w, g, pairs, rot, epsilon, v);
+  u32x4 out[4];
+  pack_bf16x32(v, out);
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      x[8 * j + 2 * e] = bf16_lo(raw[j][e]);
-      x[8 * j + 2 * e + 1] = bf16_hi(raw[j][e]);
-    }
-  float pp[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    float s = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) s = fmaf(x[4 * k + e], x[4 * k + e], s);
-    pp[k] = s;
-  }
-  float ss = ((pp[0] + pp[1]) + (pp[2] + pp[3])) + ((pp[4] + pp[5]) + (pp[6] + pp[7]));
-  ss += dpp<kDppXor1>(ss);
-  ss += dpp<kDppXor2>(ss);
-  ss += dpp<kDppHalfMirror>(ss);
-  const float scale = 1.0f / sqrtf(ss * (1.0f / 256.0f) + epsilon);
-  float w[32];
-  if (weight_f32) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float4 t = reinterpret_cast<const float4 *>(weight)[8 * g + k];
-      w[4 * k] = t.x; w[4 * k + 1] = t.y; w[4 * k + 2] = t.z; w[4 * k + 3] = t.w;
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const u32x4 t = reinterpret_cast<const u32x4 *>(weight)[4 * g + k];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        w[8 * k + 2 * e] = bf16_lo(t[e]);
-        w[8 * k + 2 * e + 1] = bf16_hi(t[e]);
-      }
-    }
-  }
-  float v[32];
-#pragma unroll
-  for (int i = 0; i < 32; ++i) v[i] = x[i] * scale * w[i];
-  const int pg = pairs / 32; // lane groups between a dim and its partner
-  const bool rotated = g < 2 * pg, first = g < pg;
-  // Partner lane: g xor 1 (pg = 1) or g xor 2 (pg = 2) among the row's
-  // lanes, by DPP; other widths through the LDS crossbar.
-  float pv[32];
-  if (pg == 1) {
-#pragma unroll
-    for (int i = 0; i < 32; ++i) pv[i] = dpp<kDppXor1>(v[i]);
-  } else if (pg == 2) {
-#pragma unroll
-    for (int i = 0; i < 32; ++i) pv[i] = dpp<kDppXor2>(v[i]);
-  } else {
-    const int lane = threadIdx.x & 63;
-    const int src_lane = first ? lane + pg : lane - pg;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) pv[i] = __shfl(v[i], src_lane);
-  }
-  if (rotated) {
-    // cos and sin of pairs p0 .. p0+31: 16-byte aligned (pairs and p0 are
-    // multiples of 32), read as 16 vectors before any is used.
-    const int p0 = 32 * (first ? g : g - pg);
-    float4 cs4[8], sn4[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      cs4[k] = reinterpret_cast<const float4 *>(rot + p0)[k];
-      sn4[k] = reinterpret_cast<const float4 *>(rot + pairs + p0)[k];
-    }
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const float4 &c4 = cs4[i >> 2], &s4 = sn4[i >> 2];
-      const float c = (i & 3) == 0 ? c4.x : (i & 3) == 1 ? c4.y : (i & 3) == 2 ? c4.z : c4.w;
-      const float sn = (i & 3) == 0 ? s4.x : (i & 3) == 1 ? s4.y : (i & 3) == 2 ? s4.z : s4.w;
-      v[i] = first ? v[i] * c - pv[i] * sn : pv[i] * sn + v[i] * c;
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    *reinterpret_cast<u32x4 *>(row + (((4 * g + j) ^ swz(r)) << 3)) =
-        u32x4{pack_bf16x2(v[8 * j], v[8 * j + 1]), pack_bf16x2(v[8 * j + 2], v[8 * j + 3]),
-              pack_bf16x2(v[8 * j + 4], v[8 * j + 5]), pack_bf16x2(v[8 * j + 6], v[8 * j + 7])};
+  for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4 *>(row + (((4 * g + j) ^ swz(r)) << 3)) = out[j];
 }
 
 // Lane-wise form (any rotary width): rows 8w .. 8w+7 one at a time, lane l
