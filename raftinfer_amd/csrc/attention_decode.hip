@@ -398,6 +398,11 @@ constexpr int kSplitDs = 4, kSplitWaves = 8;
 // per call); with sliced dims 32-token steps are as fast or faster.
 constexpr int split_chunk(int ds) { return ds == 1 ? 16 : 32; }
 constexpr int kSingleDs = 16, kSingleMfmaWaves = 8;
+// Tokens per wave step of the register-fed single-block scan: 16 rather than
+// 32 halves the registers a step holds (ctx 512 cold 8.5 -> 8.15 us, hot
+// 7.25 -> 6.95 us; 16 waves per workgroup measured slower).  The LDS-staged
+// scan keeps 32-token chunks.
+constexpr int kSingleChunk = 16;
 
 // Copies the new token's K and V rows of kv_head into the cache (bf16 to
 // bf16, so the stored bits equal the RNE cast of the reference's append).
@@ -510,14 +515,14 @@ __device__ __forceinline__ void append_rows_fused(const DecodeMfmaArgs &a, const
 // gate: element (head h, dim d) at gate[h * gate_stride + d] (gate_stride 256
 // for a split gate, 512 for the gate half of a q projection row).
 // Single-block workgroup `block` at `position` (ctx = position + 1).
-template <int DS, int WAVES, bool kFused, bool kDma = false>
+template <int DS, int WAVES, bool kFused, bool kDma = false, int CT = 32>
 __device__ __forceinline__ void single_block_body(unsigned block, const DecodeMfmaArgs &a,
                                                   const bf16_bits *__restrict__ gate,
                                                   std::size_t gate_stride,
                                                   bf16_bits *__restrict__ output,
                                                   std::size_t position, const FusedNormRope &f,
-                                                  DecodeMfmaShared<DS, WAVES> &sh, DecodeFusedQK &fq,
-                                                  DecodeStage<DS, WAVES> *stage = nullptr) {
+                                                  DecodeMfmaShared<DS, WAVES, CT> &sh, DecodeFusedQK &fq,
+                                                  DecodeStage<DS, WAVES, CT> *stage = nullptr) {
   constexpr int DIMS = kHeadDim / DS;
   const std::size_t ctx = position + 1;
   std::size_t kv_head;
@@ -545,7 +550,7 @@ __device__ __forceinline__ void single_block_body(unsigned block, const DecodeMf
     }
   }
   if constexpr (kFused) fused_qk_prologue(f, kv_head, position, fq);
-  decode_mfma_scan<DS, WAVES, 32, kFused, kDma>(a, kv_head, dq, 0, ctx, position, sh, &fq, stage);
+  decode_mfma_scan<DS, WAVES, CT, kFused, kDma>(a, kv_head, dq, 0, ctx, position, sh, &fq, stage);
   __syncthreads();
   // The scan read the new row from key/value; the cache copy goes last so its
   // load latency is not on the critical path.
@@ -574,7 +579,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_single_mfma_kernel(
     DecodeMfmaArgs a, const bf16_bits *__restrict__ gate, std::size_t gate_stride,
     bf16_bits *__restrict__ output, std::size_t host_position, const std::uint32_t *device_position,
     std::size_t threshold, FusedNormRope f) {
-  __shared__ DecodeMfmaShared<DS, WAVES> sh;
+  constexpr int CT = kDma ? 32 : kSingleChunk;
+  __shared__ DecodeMfmaShared<DS, WAVES, CT> sh;
   __shared__ DecodeFusedQK fq;
   using Stage = std::conditional_t<kDma, DecodeStage<DS, WAVES>, char>;
   __shared__ Stage stage;
@@ -585,7 +591,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_single_mfma_kernel(
     single_block_body<DS, WAVES, kFused, true>(blockIdx.x, a, gate, gate_stride, output, position, f, sh, fq,
                                                &stage);
   else
-    single_block_body<DS, WAVES, kFused, false>(blockIdx.x, a, gate, gate_stride, output, position, f, sh, fq);
+    single_block_body<DS, WAVES, kFused, false, CT>(blockIdx.x, a, gate, gate_stride, output, position, f, sh, fq);
 }
 
 // Split-K partition workgroup `block` at `position`.
@@ -673,14 +679,14 @@ __global__ __launch_bounds__(WAVES * 64) void decode_dynamic_mfma_kernel(
     float *__restrict__ pval, const std::uint32_t *device_position, std::size_t capacity,
     std::size_t max_partitions, std::size_t partition_tokens, std::size_t threshold,
     FusedNormRope f) {
-  __shared__ DecodeMfmaShared<kSingleDs, WAVES> ssh;
+  __shared__ DecodeMfmaShared<kSingleDs, WAVES, kSingleChunk> ssh;
   __shared__ DecodeMfmaShared<DS, WAVES, split_chunk(DS)> psh;
   __shared__ DecodeFusedQK fq;
   const std::size_t position = *device_position;
   if (position >= a.max_ctx) return;
   if (position + 1 < threshold)
-    single_block_body<kSingleDs, WAVES, kFused>(blockIdx.x, a, gate, gate_stride, output, position, f,
-                                                ssh, fq);
+    single_block_body<kSingleDs, WAVES, kFused, false, kSingleChunk>(blockIdx.x, a, gate, gate_stride, output,
+                                                                      position, f, ssh, fq);
   else
     split_body<DS, WAVES, split_chunk(DS), kFused>(blockIdx.x, a, pmax, psum, pval, position, capacity,
                                       max_partitions, partition_tokens, f, psh, fq);
