@@ -529,6 +529,8 @@ __device__ __forceinline__ void single_block_body(unsigned block, const DecodeMf
   int dq;
   xcd_unit<DS>(block, kv_head, dq);
   if (kv_head >= kKvHeads) return;
+  __shared__ unsigned prefetch_sink[64];
+  prefetch_head_rows<DS, WAVES>(a, kv_head, dq, ctx, lds_address(&prefetch_sink[0]));
   // The gate values of this thread's outputs are loaded before the scan, so
   // the epilogue does not wait for a load round trip of its own.
   // kDma: unconditional (index clamped) with the raw bits kept until the

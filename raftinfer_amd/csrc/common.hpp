@@ -222,6 +222,22 @@ __device__ __forceinline__ void load_lds_b128(const void *base, std::uint32_t vo
                : "memory", "m0");
 #pragma clang diagnostic pop
 }
+// 4 bytes from base + voff (per lane) into LDS at lds + 4 * lane
+// (global_load_lds_dword); the same conventions as load_lds_b128.
+__device__ __forceinline__ void load_lds_b32(const void *base, std::uint32_t voff, unsigned lds) {
+  const auto b = reinterpret_cast<std::uintptr_t>(base);
+  const auto hi = static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<std::uint32_t>(b >> 32)));
+  const auto lo = static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<std::uint32_t>(b)));
+  const std::uint64_t sbase = (static_cast<std::uint64_t>(hi) << 32) | lo;
+  const auto slds = static_cast<unsigned>(__builtin_amdgcn_readfirstlane(lds));
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2"
+               :
+               : "s"(slds), "v"(voff), "s"(sbase)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
 template <int N> __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }

@@ -444,6 +444,45 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
   }
 }
 
+// Cold-cache prefetch for the single-block scan, whose DS sibling workgroups
+// all stream the same K rows chunk by chunk (only ~128 tokens of a head in
+// flight at a time).  Each sibling first touches 1/DS of the head's K and V
+// rows of tokens [0, ctx), one dword per 128-byte line (which brings the whole
+// line into L2; a touch per 64 or 32 bytes measured no faster cold and slower
+// hot), dropped into a dummy LDS word per lane (sink), so the whole head is
+// requested from HBM at once and the scan's loads then hit L2: ctx 512 cold
+// 8.58 -> 8.25 us, ctx 1024 13.9 -> 12.25 us; hot it costs 0.2-0.3 us.  At
+// most kRounds instructions per wave (all of ctx <= 2048 at 8 waves, DS = 16).
+// These loads are older than every load of the scan, so its in-order vmcnt
+// waits still name the same loads.  Head-major caches only (a token-major
+// head is not contiguous).
+template <int DS, int WAVES, int kRounds = 2>
+__device__ __forceinline__ void prefetch_head_rows(const DecodeMfmaArgs &a, std::size_t kv_head, int dq,
+                                                   std::size_t ctx, unsigned sink) {
+  if (!a.head_major) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  constexpr std::size_t kLine = 128;                   // one touch per 128-byte line
+  constexpr std::size_t kPieces = kHeadDim * 2 / kLine; // lines per row
+  const std::size_t pieces = ctx * kPieces;          // per plane
+  const std::size_t per = (pieces + DS - 1) / DS;    // per sibling and plane
+  const std::size_t blocks = (per + 63) / 64;        // instructions per plane
+  const std::size_t lim = (static_cast<std::size_t>(dq) + 1) * per < pieces
+                              ? (static_cast<std::size_t>(dq) + 1) * per
+                              : pieces;
+  const bf16_bits *kb = a.cache + cache_row(true, 0, kv_head, a.max_ctx);
+  const bf16_bits *vb = kb + a.max_ctx * kKvHeads * kHeadDim;
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const std::size_t i = static_cast<std::size_t>(wave) + static_cast<std::size_t>(r) * WAVES;
+    if (i >= 2 * blocks) break; // wave-uniform
+    const bool second = i >= blocks;
+    std::size_t piece = static_cast<std::size_t>(dq) * per + (second ? i - blocks : i) * 64 + lane;
+    piece = piece < lim ? piece : lim - 1;
+    load_lds_b32(second ? vb : kb, static_cast<std::uint32_t>(piece * kLine), sink);
+  }
+}
+
 template <int DS, int WAVES, int CT>
 __device__ __forceinline__ void decode_mfma_combine(const DecodeMfmaShared<DS, WAVES, CT> &sh, int h,
                                                     int d, float &m_out, float &l_out,
