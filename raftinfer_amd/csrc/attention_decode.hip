@@ -777,16 +777,17 @@ void launch_decode_mfma(const DecodeMfmaArgs &args, const bf16_bits *g, std::siz
     return;
   }
   if (!partition_only && (dynamic || single || host_ctx < plan.split_k_threshold_tokens)) {
-    // Above two chunks per wave the LDS-staged scan streams the next chunk
-    // under the current one (ctx 1024: 11.2 -> 10.3 us hot); at ctx <= 512
-    // the register-fed scan is as fast or faster cold.
+    // Above 1.5 chunks per wave the LDS-staged scan streams the next chunk
+    // under the current one (ctx 1024: 11.2 -> 10.3 us hot; with the
+    // cold-cache prefetch, ctx 512 cold 8.23 -> 8.06 us, hot 6.93 -> 6.86);
+    // at ctx 320 the register-fed scan is faster (6.65 against 6.75 us cold).
     // (The stage's LDS-direct loads of the new row need 16-byte aligned
     // key / value rows; other pointers take the register-fed scan.)
     const std::size_t ctx_bound = dynamic ? shape.max_context_tokens : host_ctx;
     const bool rows_aligned =
         ((reinterpret_cast<std::uintptr_t>(args.key_new) | reinterpret_cast<std::uintptr_t>(args.value_new)) &
          15u) == 0;
-    if (ctx_bound > 2 * kSingleMfmaWaves * 32 && rows_aligned)
+    if (2 * ctx_bound > 3 * kSingleMfmaWaves * 32 && rows_aligned)
       decode_single_mfma_kernel<kSingleDs, kSingleMfmaWaves, kFused, true>
           <<<xcd_grid<kSingleDs>(kKvHeads), kSingleMfmaWaves * 64, 0, stream>>>(
               args, g, gate_stride, out, shape.past_tokens, device_position,

@@ -166,9 +166,9 @@ def test_split_k_cfg2_long_context(gpu, ctx):
 
 
 @pytest.mark.parametrize("layout", [0, 1])
-@pytest.mark.parametrize("ctx", [513, 777, 1024, 1500])
+@pytest.mark.parametrize("ctx", [385, 512, 513, 777, 1024, 1500])
 def test_single_block_staged_scan(gpu, layout, ctx):
-    # Above 512 tokens the single-block kernel feeds its scan through an LDS
+    # Above 384 tokens the single-block kernel feeds its scan through an LDS
     # stage (the next chunk streams in under the current one); ragged last
     # chunks, both cache layouts, host and device positions.
     for device_position in (False, True):
@@ -182,7 +182,7 @@ def test_single_block_staged_scan(gpu, layout, ctx):
 
 @pytest.mark.parametrize("ctx", [1, 2, 31, 33, 100, 300])
 def test_single_block_staged_scan_short_context(gpu, ctx):
-    # A device position with max_ctx above 512 selects the staged scan whatever
+    # A device position with max_ctx above 384 selects the staged scan whatever
     # the position, so short contexts (waves with no chunk, one ragged chunk)
     # run through it too.
     out, expect, cache, keys, vals, _, _ = run_decode(3, 1, 1, ctx, 2048, mode=1, device_position=True,
