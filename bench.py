@@ -80,13 +80,21 @@ def delta_entry_bytes(T):
 
 def cpu_description():
     model = "unknown"
+    ids = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
+            key, _, val = line.partition(":")
+            key = key.strip()
+            if key == "model name" and model == "unknown":
+                model = val.strip()
+            elif key in ("cpu family", "model", "stepping") and key not in ids:
+                ids[key] = val.strip()
+            elif not line.strip() and ids:
+                break  # the first processor's block is enough
     except OSError:
         pass
+    if ids:  # a virtualised host may report only the product line as its name
+        model += " (" + ", ".join(f"{k} {v}" for k, v in ids.items()) + ")"
     try:
         avail = len(os.sched_getaffinity(0))
     except AttributeError:
