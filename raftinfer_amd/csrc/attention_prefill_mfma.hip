@@ -422,7 +422,6 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
       }
     }
     wait_lgkm0(); // the K tile has been read
-    if (more) issue_half(k_src, lds_k, k0_next, 1);
 
     // Key of accumulator register i: k0 + 8 (i / 4) + 4 half + i % 4.  Only
     // a tile that reaches past the tile's first query position is masked.
@@ -469,6 +468,7 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
                                                 pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])});
     }
 
+    if (more) issue_half(k_src, lds_k, k0_next, 1); // after the softmax
     if (first) {
       if (more) wait_vm<16 + kLateLoads>(); else wait_vm<kLateLoads>(); // V(t) has landed
     } else {
