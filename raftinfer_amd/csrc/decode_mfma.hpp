@@ -464,22 +464,24 @@ __device__ __forceinline__ void prefetch_head_rows(const DecodeMfmaArgs &a, std:
   const int wave = threadIdx.x >> 6;
   constexpr std::size_t kLine = 128;                   // one touch per 128-byte line
   constexpr std::size_t kPieces = kHeadDim * 2 / kLine; // lines per row
-  const std::size_t pieces = ctx * kPieces;          // per plane
-  const std::size_t per = (pieces + DS - 1) / DS;    // per sibling and plane
-  const std::size_t blocks = (per + 63) / 64;        // instructions per plane
-  const std::size_t lim = (static_cast<std::size_t>(dq) + 1) * per < pieces
-                              ? (static_cast<std::size_t>(dq) + 1) * per
-                              : pieces;
-  const bf16_bits *kb = a.cache + cache_row(true, 0, kv_head, a.max_ctx);
+  const std::size_t pieces = ctx * kPieces;       // per plane
+  const std::size_t per = (pieces + DS - 1) / DS; // per sibling and plane
+  const std::size_t first = static_cast<std::size_t>(dq) * per;
+  if (first >= pieces) return; // (uniform)
+  const std::size_t count = per < pieces - first ? per : pieces - first;
+  const std::size_t blocks = (count + 63) / 64; // instructions per plane
+  // The sibling's first line is folded into the (scalar) base, so the per-lane
+  // offset stays below kRounds * WAVES * 64 lines (128 KiB) at any context.
+  const bf16_bits *kb = a.cache + cache_row(true, 0, kv_head, a.max_ctx) + first * (kLine / 2);
   const bf16_bits *vb = kb + a.max_ctx * kKvHeads * kHeadDim;
 #pragma unroll
   for (int r = 0; r < kRounds; ++r) {
     const std::size_t i = static_cast<std::size_t>(wave) + static_cast<std::size_t>(r) * WAVES;
     if (i >= 2 * blocks) break; // wave-uniform
     const bool second = i >= blocks;
-    std::size_t piece = static_cast<std::size_t>(dq) * per + (second ? i - blocks : i) * 64 + lane;
-    piece = piece < lim ? piece : lim - 1;
-    load_lds_b32(second ? vb : kb, static_cast<std::uint32_t>(piece * kLine), sink);
+    std::size_t line = (second ? i - blocks : i) * 64 + lane;
+    line = line < count ? line : count - 1;
+    load_lds_b32(second ? vb : kb, static_cast<std::uint32_t>(line * kLine), sink);
   }
 }
 
