@@ -239,6 +239,7 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
        c0 += static_cast<std::size_t>(WAVES) * CT) {
     u32x4 kr[G][4];
     VRow<VEC> vv[TPL];
+    [[maybe_unused]] bool issue_second = false;
     if constexpr (kDma) {
       // The stage is used in two halves so that the next chunk streams in
       // behind this one: once rows 0-15 have landed and been read, the next
@@ -270,7 +271,7 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
       for (int j = 0; j < TPL; ++j)
         vv[j].w[0] = *reinterpret_cast<const std::uint32_t *>(&stage->v[wave][(tl + TL * j) * DIMS + VEC * dl]);
       wait_lgkm0(); // rows 16-31 and V have been read
-      if (more) dma_half(c0 + static_cast<std::size_t>(WAVES) * CT, 1);
+      issue_second = more; // goes out after the softmax, below (ctx 1024 cold 12.24 -> 11.93 us)
       if (pos >= c0 && pos < c0 + CT) { // this chunk holds the new token (wave-uniform)
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -376,6 +377,9 @@ __device__ __forceinline__ void decode_mfma_scan(const DecodeMfmaArgs &a, std::s
       }
     l_run = l_run * sc + psum;
     m_run = m_new;
+    if constexpr (kDma) {
+      if (issue_second) dma_half(c0 + static_cast<std::size_t>(WAVES) * CT, 1);
+    }
     wave_lds_order();
     float scl[4]; // lane h < 4 holds head h's rescale factor
 #pragma unroll
