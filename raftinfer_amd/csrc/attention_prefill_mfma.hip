@@ -12,9 +12,10 @@
 //   staging     K and V rows go from the cache straight into the wave's own
 //               LDS tile (global_load_lds_dwordx4, no VGPRs), stored as two
 //               halves of the head dims (4 half-rows of 256 bytes per
-//               instruction); each half of the next tile's K is issued as soon
-//               as the same half of the current K tile has been read, and V
-//               likewise (PP512 13.12 -> 12.80 us against whole-tile issue).
+//               instruction); the next tile's K goes out after the QK chain
+//               (first half) and after the softmax (second half), its V half
+//               by half as the current V tile's halves have been read (PP512
+//               13.12 -> ~12.8 us against whole-tile issue after each read).
 //               Half-rows are stored as 16 16-byte chunks with chunk c at
 //               c ^ swz(row) (see swz for the bank conflicts this leaves);
 //   S^T = K Q^T 16 x v_mfma_f32_32x32x16_bf16, K and Q rows read from LDS
@@ -416,12 +417,9 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[j], qa[j], s, 0, 0, 0);
-      if (k4 == 1) {
-        wait_lgkm0(); // the K tile's first half has been read
-        if (more) issue_half(k_src, lds_k, k0_next, 0);
-      }
     }
     wait_lgkm0(); // the K tile has been read
+    if (more) issue_half(k_src, lds_k, k0_next, 0);
 
     // Key of accumulator register i: k0 + 8 (i / 4) + 4 half + i % 4.  Only
     // a tile that reaches past the tile's first query position is masked.
