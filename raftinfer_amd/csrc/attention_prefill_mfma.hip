@@ -13,9 +13,9 @@
 //               LDS tile (global_load_lds_dwordx4, no VGPRs), stored as two
 //               halves of the head dims (4 half-rows of 256 bytes per
 //               instruction); the next tile's K goes out after the QK chain
-//               (first half) and after the softmax (second half), its V half
-//               by half as the current V tile's halves have been read (PP512
-//               13.12 -> ~12.8 us against whole-tile issue after each read).
+//               (first half) and after the softmax (second half), its V after
+//               the PV (PP512 13.12 -> ~12.8 us against whole-tile issue
+//               straight after each tile's reads).
 //               Half-rows are stored as 16 16-byte chunks with chunk c at
 //               c ^ swz(row) (see swz for the bank conflicts this leaves);
 //   S^T = K Q^T 16 x v_mfma_f32_32x32x16_bf16, K and Q rows read from LDS
@@ -51,7 +51,6 @@ constexpr int kThreads = kWaves * kWave;
 constexpr float kLazyRescale = 8.0f; // log2 units
 constexpr int kPvBatch = 8;          // PV MFMAs whose operands are read together
 constexpr int kHalfElems = kKTile * kHeadDim / 2; // one half of a K / V tile (128 dims)
-static_assert(kPvBatch == 8, "the first PV batch reads exactly dims 0-127 (the first tile half)");
 
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4v lds_short4v;
@@ -500,15 +499,11 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
           const int nb = (b0 + j) >> 1, kb = (b0 + j) & 1;
           mfma_acc_agpr(o[nb], av[j], pw[kb]);
         }
-        if (b0 == 0) {
-          wait_lgkm0(); // the V tile's first half (dims 0-127) has been read
-          if (more) issue_half(v_src, lds_v, k0_next, 0);
-        }
       }
       mfma_drain(); // the accumulators may be read by VALU code below
     }
     wait_lgkm0(); // the V tile has been read
-    if (more) issue_half(v_src, lds_v, k0_next, 1);
+    if (more) issue(v_src, lds_v, k0_next);
   }
 
 
