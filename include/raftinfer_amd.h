@@ -205,7 +205,10 @@ int raftinfer_amd_online_attention_prefill_fused(
  * array of raftinfer_amd_online_attention_static_workspace_bytes() bytes per
  * GPU (8,454,144: max_context_tokens <= 131072 at split_k_256, <= 262144 at
  * split_k_512); larger plans return RAFTINFER_AMD_INVALID_ARGUMENT.  Calls
- * that overlap on one GPU share that array and race. */
+ * that overlap on one GPU share that array and race.  The first call on each
+ * device looks up the array's address and must not be under stream capture
+ * (it returns RAFTINFER_AMD_INVALID_ARGUMENT there); later calls may be
+ * captured. */
 size_t raftinfer_amd_online_attention_static_workspace_bytes(void);
 int raftinfer_amd_online_attention_decode_static_workspace(
     const void *query, const void *key, const void *value, const void *gate, void *output,

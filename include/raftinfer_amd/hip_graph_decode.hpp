@@ -8,7 +8,9 @@
 // reference executor builds around it (cpp/execution/qwen35_executor.cu:
 // 2191-2226): one variant for the single-block plan of short contexts, then
 // one per distinct qwen35_online_decode_plan over the positions from the
-// split threshold - 1 to max_context - 1.  Each variant holds one captured
+// split threshold - 1 to max_context - 1 (split_k_256 / split_k_512 only:
+// auto_select and single_block keep the single-block variant at every
+// position, as the reference's table does).  Each variant holds one captured
 // decode-attention step (qwen35_online_attention_decode with that plan and a
 // device-resident position), so a serving loop writes the position on the
 // device and replays the variant of the current position.

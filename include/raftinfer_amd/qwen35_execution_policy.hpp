@@ -1,5 +1,5 @@
 // Execution-policy enums, unchanged from the reference
-// (cpp/execution/qwen35_execution_policy.hpp:7-38) so callers keep their
+// (cpp/execution/qwen35_execution_policy.hpp:7-41) so callers keep their
 // policy values and switch statements.
 #pragma once
 
@@ -37,5 +37,11 @@ struct Qwen35ExecutionPolicy {
   bool decode_graph{true};
   bool grouped_input_casts{true};
 };
+
+// Declared as the reference declares it (qwen35_execution_policy.hpp:40-41);
+// the definition stays with the caller's session code (the reference's
+// cpp/execution/session.cpp:17-37 reads RAFTINFER_QWEN35_DECODE_ATTENTION).
+// Nothing in this library defines or calls it.
+Qwen35ExecutionPolicy qwen35_execution_policy_from_environment(Qwen35ExecutionPolicy policy);
 
 } // namespace raftinfer

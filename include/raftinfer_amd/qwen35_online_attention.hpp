@@ -145,7 +145,9 @@ void qwen35_online_attention_prefill_fused(const void *query_gate, const void *k
 // max_context_tokens <= 131072 at split_k_256, <= 262144 at split_k_512); a
 // larger plan is rejected with Qwen35PrimitiveError.  Nothing is allocated.
 // Every call on one GPU shares that array, so calls that overlap on one GPU
-// (different streams, or different host threads) race; serialize them.
+// (different streams, or different host threads) race; serialize them.  The
+// first call on each device looks up the array's address and must not be
+// under stream capture (it throws there); later calls may be captured.
 std::size_t qwen35_online_attention_static_workspace_bytes() noexcept;
 void qwen35_online_attention_decode_static_workspace(
     const void *query, const void *key, const void *value, const void *gate, void *output,

@@ -1104,12 +1104,19 @@ void *g_scratch_ptr[kMaxDevices] = {};
 
 // The current device's address of `scratch`, looked up once per device with
 // that device current.
-void *scratch_for_current_device() {
+void *scratch_for_current_device(hipStream_t stream) {
   int device = -1;
   require<Err>(hipGetDevice(&device) == hipSuccess, "static decode workspace: hipGetDevice failed");
   require<Err>(device >= 0 && device < kMaxDevices, "static decode workspace: device index out of range");
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (g_scratch_ptr[device] == nullptr) {
+    // The lookup is not a stream operation, but it may load the code object;
+    // it is done outside any capture so that a captured call never depends on it.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    require<Err>(hipStreamIsCapturing(stream, &capture) == hipSuccess &&
+                     capture == hipStreamCaptureStatusNone,
+                 "static decode workspace: the first call on a device must not be captured "
+                 "(call it once eagerly on this device before capturing it)");
     void *ptr = nullptr;
     const hipError_t rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     require<Err>(rc == hipSuccess && ptr != nullptr,
@@ -1142,7 +1149,7 @@ void qwen35_online_attention_decode_static_workspace(
                  "131072 tokens at split_k_256, 262144 at split_k_512); pass a workspace to "
                  "qwen35_online_attention_decode instead");
   }
-  void *workspace = bytes != 0 ? scratch_for_current_device() : nullptr;
+  void *workspace = bytes != 0 ? scratch_for_current_device(stream) : nullptr;
   decode_impl(query, key, value, gate, output, kv_cache, kv_cache_bytes, workspace, bytes, shape,
               activation_dtype, cache_dtype, cache_layout, plan, device_position, stream, false);
 }

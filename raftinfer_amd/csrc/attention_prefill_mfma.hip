@@ -457,12 +457,18 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
     for (int kb = 0; kb < 2; ++kb) {
       float p[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        p[j] = fexp2(s[8 * kb + j] - m_ref);
-        l_run += p[j];
+      for (int j = 0; j < 8; ++j) p[j] = fexp2(s[8 * kb + j] - m_ref);
+      const u32x4 pk{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                     pack_bf16x2(p[6], p[7])};
+      // The sum takes the same bf16 probabilities the PV product uses, so the
+      // output is an exact convex combination of the V rows with those weights
+      // (a key that holds all the weight gives its V row exactly).
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const std::uint32_t w = pk[j];
+        l_run += bf16_lo(w) + bf16_hi(w);
       }
-      pw[kb] = __builtin_bit_cast(bf16x8, u32x4{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
-                                                pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])});
+      pw[kb] = __builtin_bit_cast(bf16x8, pk);
     }
 
     if (more) issue_half(k_src, lds_k, k0_next, 1); // after the softmax

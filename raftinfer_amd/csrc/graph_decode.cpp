@@ -101,11 +101,11 @@ Qwen35DecodeAttentionGraphs::Qwen35DecodeAttentionGraphs(
   by_position_.assign(max_ctx, 0);
   variants_.push_back({qwen35_online_decode_plan(shape_at(0), Qwen35DecodeAttentionMode::single_block, 1),
                        std::make_unique<HipGraphDecode>(device_id, stream)});
-  const Qwen35DecodeAttentionMode resolved =
-      mode == Qwen35DecodeAttentionMode::auto_select ? Qwen35DecodeAttentionMode::split_k_256 : mode;
-  const std::size_t threshold = resolved == Qwen35DecodeAttentionMode::split_k_256   ? 256
-                                : resolved == Qwen35DecodeAttentionMode::split_k_512 ? 512
-                                                                                     : 0;
+  // As the reference executor: only the explicit split modes add split-K
+  // variants; auto_select and single_block replay variant 0 at every position.
+  const std::size_t threshold = mode == Qwen35DecodeAttentionMode::split_k_256   ? 256
+                                : mode == Qwen35DecodeAttentionMode::split_k_512 ? 512
+                                                                                 : 0;
   if (threshold != 0) {
     std::size_t active = 0;
     for (std::size_t position = threshold - 1; position < max_ctx; ++position) {
@@ -146,7 +146,7 @@ const Qwen35OnlineDecodePlan &Qwen35DecodeAttentionGraphs::plan_for(std::size_t 
 }
 
 void Qwen35DecodeAttentionGraphs::replay(std::size_t position) {
-  variants_[variant_for(position)].graph->replay_on_current_device();
+  variants_[variant_for(position)].graph->replay(); // selects the capture device
 }
 
 } // namespace kernels

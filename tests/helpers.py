@@ -72,16 +72,25 @@ def read_cache(cache, layout, n, max_ctx, hkv=HKV, d=D):
     return c[0, :n], c[1, :n]
 
 
-def assert_bf16_close(actual, expected, max_abs=1e-2, rel_l2=5e-3, what=""):
-    """The bf16-output gate: every element within max(max_abs, one bf16 ulp of
-    the expected value) and the whole tensor within rel_l2 (relative L2)."""
+def assert_bf16_close(actual, expected, max_abs=1e-2, rel_l2=5e-3, what="", both_bf16=False):
+    """The bf16-output gate of the fp32-accumulated reference: every element
+    within max_abs and the whole tensor within rel_l2 (relative L2).
+
+    `expected` is the oracle's fp32 output, not rounded.  Only where the bf16
+    grid itself is coarser than the gate (|e| >= 4, where half an ulp of bf16 is
+    1.56e-2 and no bf16 value need lie within 1e-2 of e) does an element get
+    half an ulp of e plus 2e-3 instead; below |e| = 4 the bound is max_abs
+    exactly.  both_bf16: `expected` is itself a bf16 result (one GPU path
+    against another), so the two may sit one bf16 ulp of e apart."""
     a = np.asarray(actual, np.float64).ravel()
     e = np.asarray(expected, np.float64).ravel()
     assert np.all(np.isfinite(a)), f"{what}: non-finite output"
     ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(e), 1e-30))) - 7)
+    grid = ulp if both_bf16 else 0.5 * ulp + 2e-3
     err = np.abs(a - e)
-    bad = err > np.maximum(max_abs, ulp)
-    assert not bad.any(), f"{what}: {bad.sum()} elements off, worst {err.max():.3e}"
+    bad = err > np.maximum(max_abs, grid)
+    assert not bad.any(), (f"{what}: {bad.sum()} elements off, worst {err.max():.3e} "
+                           f"at expected {e[np.argmax(err)]:.4f}")
     r = np.linalg.norm(a - e) / max(np.linalg.norm(e), 1e-30)
     assert r <= rel_l2, f"{what}: rel-L2 {r:.3e} > {rel_l2}"
 

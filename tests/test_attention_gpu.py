@@ -75,7 +75,7 @@ def test_decode_cfg1_single_block_ctx512(gpu):
     # benchmark config 1: ctx 512, bf16 head-major cache, single-block, no split.
     out, expect, cache, keys, vals, _, _ = run_decode(3, 1, 1, 512, 512, mode=None,
                                                       device_position=False, seed=11)
-    assert_bf16_close(out, bf16(expect), what="cfg1 decode")
+    assert_bf16_close(out, expect, what="cfg1 decode")
     ck, cv = read_cache(cache, 1, 512, 512)
     assert np.array_equal(ck, keys) and np.array_equal(cv, vals)  # append is bit-exact
 
@@ -87,7 +87,7 @@ def test_prefill_mfma_key_tile_past_first_query(gpu, T, past):
     # columns; their probabilities must be 0, not exp2(-inf + inf) = NaN.
     out, expect, *_ = run_prefill(3, 1, 1, T, HQ, HKV, D, past, seed=T * 1000 + past)
     assert np.isfinite(out).all()
-    assert_bf16_close(out, bf16(expect), what=f"prefill T={T} past={past}")
+    assert_bf16_close(out, expect, what=f"prefill T={T} past={past}")
 
 
 @pytest.mark.parametrize("layout", [0, 1])
@@ -111,7 +111,7 @@ def test_split_k_256_boundaries_and_partials(gpu, ctx):
     out, expect, cache, keys, vals, ws, plan = run_decode(3, 1, 1, ctx, max_ctx, mode=2, seed=ctx,
                                                           ws_fill=0xA5)
     assert close_enough(out, expect)
-    assert_bf16_close(out, bf16(expect), what=f"split-256 ctx {ctx}")
+    assert_bf16_close(out, expect, what=f"split-256 ctx {ctx}")
     wsb = ws.cpu().numpy()
     if ctx < plan[2]:
         assert np.all(wsb == 0xA5)  # below the threshold the workspace is untouched
@@ -138,7 +138,7 @@ def test_split_k_256_layout_sweep(gpu, layout, ctx):
     # capacity above the active partitions (max_ctx 4096), device position, ~1% heavy rows.
     out, expect, cache, keys, vals, *_ = run_decode(3, 1, layout, ctx, 4096, mode=2, seed=ctx + 31 * layout,
                                                     heavy_rows=0.01)
-    assert_bf16_close(out, bf16(expect), what=f"split-256 layout {layout} ctx {ctx}")
+    assert_bf16_close(out, expect, what=f"split-256 layout {layout} ctx {ctx}")
     ck, cv = read_cache(cache, layout, ctx, 4096)
     assert np.array_equal(ck, keys) and np.array_equal(cv, vals)
 
@@ -148,7 +148,7 @@ def test_split_k_row_merge_sparse_waves(gpu, ctx):
     # max_ctx 16384 gives a plan capacity of 64 partitions, so the 8-wave row merge runs;
     # at ctx 2 and 300 (1-2 active partitions) most of its waves have no partition.
     out, expect, *_ = run_decode(3, 1, 1, ctx, 16384, mode=2, seed=ctx + 7, heavy_rows=0.01)
-    assert_bf16_close(out, bf16(expect), what=f"row merge ctx {ctx}")
+    assert_bf16_close(out, expect, what=f"row merge ctx {ctx}")
 
 
 @pytest.mark.parametrize("ctx", [513, 777])
@@ -162,7 +162,7 @@ def test_split_k_cfg2_long_context(gpu, ctx):
     # benchmark config 2: auto (split-K 256), ~1% of K rows x8, host position.
     out, expect, *_ = run_decode(3, 1, 1, ctx, ctx, mode=0, device_position=False, seed=ctx,
                                  heavy_rows=0.01)
-    assert_bf16_close(out, bf16(expect), what=f"cfg2 ctx {ctx}")
+    assert_bf16_close(out, expect, what=f"cfg2 ctx {ctx}")
 
 
 @pytest.mark.parametrize("layout", [0, 1])
@@ -175,7 +175,7 @@ def test_single_block_staged_scan(gpu, layout, ctx):
         out, expect, cache, keys, vals, _, _ = run_decode(3, 1, layout, ctx, ctx + 7, mode=1,
                                                           device_position=device_position,
                                                           seed=ctx * 3 + layout, heavy_rows=0.01)
-        assert_bf16_close(out, bf16(expect), what=f"single-block ctx {ctx} layout {layout}")
+        assert_bf16_close(out, expect, what=f"single-block ctx {ctx} layout {layout}")
         ck, cv = read_cache(cache, layout, ctx, ctx + 7)
         assert np.array_equal(ck, keys) and np.array_equal(cv, vals)
 
@@ -187,7 +187,7 @@ def test_single_block_staged_scan_short_context(gpu, ctx):
     # run through it too.
     out, expect, cache, keys, vals, _, _ = run_decode(3, 1, 1, ctx, 2048, mode=1, device_position=True,
                                                       seed=ctx + 4000, heavy_rows=0.01)
-    assert_bf16_close(out, bf16(expect), what=f"staged single-block ctx {ctx}")
+    assert_bf16_close(out, expect, what=f"staged single-block ctx {ctx}")
     ck, cv = read_cache(cache, 1, ctx, 2048)
     assert np.array_equal(ck, keys) and np.array_equal(cv, vals)
 
@@ -195,7 +195,7 @@ def test_single_block_staged_scan_short_context(gpu, ctx):
 def test_single_block_equals_split(gpu):
     a, *_ = run_decode(3, 1, 1, 1500, 2048, mode=1, seed=99)
     b, *_ = run_decode(3, 1, 1, 1500, 2048, mode=2, seed=99)
-    assert_bf16_close(a, b, what="single vs split")
+    assert_bf16_close(a, b, what="single vs split", both_bf16=True)
 
 
 def test_capacity_guard_reports_instead_of_trapping(gpu):
@@ -250,7 +250,7 @@ def test_split_k_row_merge_multi_chunk(gpu, ctx):
     keys = bf16(np.concatenate([past_k, ka[None]]))
     vals = bf16(np.concatenate([past_v, va[None]]))
     expect = orc.attention_core(qa[None], keys, vals, ga[None], ctx - 1)[0]
-    assert_bf16_close(from_dev(out).reshape(HQ, D), bf16(expect), what=f"row merge ctx {ctx}")
+    assert_bf16_close(from_dev(out).reshape(HQ, D), expect, what=f"row merge ctx {ctx}")
 
 
 def prefill_case(act, cdt, layout, T, hq, hkv, d, past, seed, q_scale=1.0):
@@ -292,7 +292,7 @@ def run_prefill(act, cdt, layout, T, hq, hkv, d, past, seed=0, inputs=None):
 def test_prefill_mfma_model_shape(gpu, T, past):
     # benchmark config 3 (PP128 / PP512) and the reference's {17,16,4,256,111} case.
     out, expect, cache, keys, vals = run_prefill(3, 1, 1, T, HQ, HKV, D, past, seed=T + past)
-    assert_bf16_close(out, bf16(expect), what=f"prefill T={T} past={past}")
+    assert_bf16_close(out, expect, what=f"prefill T={T} past={past}")
     ck, cv = read_cache(cache, 1, past + T, past + T)
     assert np.array_equal(ck, keys) and np.array_equal(cv, vals)
 
@@ -305,7 +305,7 @@ def test_prefill_mfma_ragged_sweep(gpu, T, past):
     # (with past == 0 the kernel also writes the cache rows itself).
     out, expect, cache, keys, vals = run_prefill(3, 1, 1, T, HQ, HKV, D, past, seed=7 * T + past)
     assert np.isfinite(out).all()
-    assert_bf16_close(out, bf16(expect), what=f"prefill T={T} past={past}")
+    assert_bf16_close(out, expect, what=f"prefill T={T} past={past}")
     ck, cv = read_cache(cache, 1, past + T, past + T)
     assert np.array_equal(ck, keys) and np.array_equal(cv, vals)
 
@@ -376,7 +376,7 @@ def test_prefill_mfma_adversarial_rescaling_model_shape(gpu, direction, past):
     out, expect, *_ = run_prefill(3, 1, 1, T, HQ, HKV, D, past,
                                   inputs=(q, g, kall[past:], vall[past:], kall[:past], vall[:past]))
     assert np.isfinite(out).all()
-    assert_bf16_close(out, bf16(expect), what=f"adversarial ramp dir {direction} past {past}")
+    assert_bf16_close(out, expect, what=f"adversarial ramp dir {direction} past {past}")
 
 
 def test_prefill_mfma_pp2048_vs_torch_fp32(gpu):
@@ -398,7 +398,7 @@ def test_prefill_mfma_pp2048_vs_torch_fp32(gpu):
     s = torch.matmul(qf, kf.transpose(1, 2)) / 16.0
     s = s.masked_fill(torch.triu(torch.ones(T, T, device="cuda", dtype=torch.bool), 1), float("-inf"))
     ref = torch.matmul(torch.softmax(s, dim=-1), vf).permute(1, 0, 2) * torch.sigmoid(g.float())
-    assert_bf16_close(from_dev(out), bf16(from_dev(ref)), what="PP2048 vs torch fp32")
+    assert_bf16_close(from_dev(out), from_dev(ref), what="PP2048 vs torch fp32")
 
 
 @pytest.mark.parametrize("act", [1, 2, 3])
@@ -460,7 +460,7 @@ def test_batched_ragged_decode(gpu, lengths, max_ctx):
     torch.cuda.synchronize()
     got = from_dev(out)
     for b in range(B):
-        assert_bf16_close(got[b], bf16(expects[b]), what=f"batched seq {b} len {lengths[b]}")
+        assert_bf16_close(got[b], expects[b], what=f"batched seq {b} len {lengths[b]}")
 
 
 @pytest.mark.parametrize("act", [1, 3])
@@ -537,11 +537,11 @@ def test_batched_ragged_decode_cfg4_full_size(gpu):
                                            one, cache[b * per:(b + 1) * per], ws1, shape, 3, 1, 1,
                                            plan=plan)
         torch.cuda.synchronize()
-        assert_bf16_close(got[b], from_dev(one).reshape(HQ, D), what=f"cfg4 seq {b} len {L} vs single")
+        assert_bf16_close(got[b], from_dev(one).reshape(HQ, D), what=f"cfg4 seq {b} len {L} vs single", both_bf16=True)
     order = np.argsort(lengths)
     for b in {int(order[0]), int(order[-1]), int(order[len(order) // 3]), int(order[2 * len(order) // 3])}:
         L = int(lengths[b])
         c = from_dev(cache[b * per:(b + 1) * per]).reshape(2, HKV, max_ctx, D)[:, :, :L]
         keys, vals = c[0].transpose(1, 0, 2), c[1].transpose(1, 0, 2)
         expect = orc.attention_core(from_dev(q[b])[None], keys, vals, from_dev(g[b])[None], L - 1)[0]
-        assert_bf16_close(got[b], bf16(expect), what=f"cfg4 seq {b} len {L} vs oracle")
+        assert_bf16_close(got[b], expect, what=f"cfg4 seq {b} len {L} vs oracle")

@@ -97,9 +97,9 @@ def test_fused_decode_against_oracle(gpu):
     keys = np.concatenate([c["past_k"], kb[None]])
     vals = np.concatenate([c["past_v"], c["v"][None]])
     want = orc.attention_core(bf16(q), keys, vals, c["qg"][None, :, 1], ctx - 1)[0]
-    assert_bf16_close(from_dev(c["out2"]).reshape(HQ, D), bf16(want), what="fused decode")
+    assert_bf16_close(from_dev(c["out2"]).reshape(HQ, D), want, what="fused decode")
     ck, _ = read_cache(from_dev(c["cache2"]), 1, ctx, 4096)
-    assert_bf16_close(ck[ctx - 1], kb, what="appended k")
+    assert_bf16_close(ck[ctx - 1], kb, what="appended k", both_bf16=True)
 
 
 def _prefill_case(T, past, rot, wdt, layout, seed):
@@ -161,7 +161,7 @@ def test_fused_prefill_against_oracle(gpu):
     keys = np.concatenate([c["pk"], k])
     vals = np.concatenate([c["pv"], c["v"]])
     want = orc.attention_core(q, keys, vals, c["qg"][:, :, 1], past)
-    assert_bf16_close(from_dev(c["out2"]).reshape(T, HQ, D), bf16(want), what="fused prefill")
+    assert_bf16_close(from_dev(c["out2"]).reshape(T, HQ, D), want, what="fused prefill")
     ck, cv = read_cache(from_dev(c["cache2"]), 1, past + T, past + T)
-    assert_bf16_close(ck[past:], k, what="appended k")
+    assert_bf16_close(ck[past:], k, what="appended k", both_bf16=True)
     assert np.array_equal(cv[past:], c["v"])

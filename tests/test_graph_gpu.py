@@ -195,5 +195,22 @@ def test_decode_graph_variants_across_bucket_boundaries(gpu):
         torch.cuda.synchronize()
         want = orc.attention_core(q_np[None], keys[:position + 1], vals[:position + 1], g_np[None],
                                   position)[0]
-        assert_bf16_close(from_dev(out).reshape(HQ, D), bf16(want), what=f"graph position {position}")
+        assert_bf16_close(from_dev(out).reshape(HQ, D), want, what=f"graph position {position}")
     graphs.close()
+    # auto_select and single_block build only the single-block variant, as the reference
+    # executor does (qwen35_executor.cu:2199-2205: threshold 0), and replay it at any position.
+    for mode in (ops.AUTO, ops.SINGLE_BLOCK):
+        g2 = ops.Qwen35DecodeAttentionGraphs(shape, mode, 3, 1, 1, q, k_in, v_in, g, out, cache, ws,
+                                             pos, stream=gpu)
+        assert g2.variant_count() == 1
+        assert [g2.variant_for(p) for p in (0, 255, 511, 1099)] == [0, 0, 0, 0]
+        position = 700
+        k_in.copy_(to_dev(keys[position], torch.bfloat16).flatten())
+        v_in.copy_(to_dev(vals[position], torch.bfloat16).flatten())
+        pos.fill_(position)
+        g2.replay(position)
+        torch.cuda.synchronize()
+        want = orc.attention_core(q_np[None], keys[:position + 1], vals[:position + 1], g_np[None],
+                                  position)[0]
+        assert_bf16_close(from_dev(out).reshape(HQ, D), want, what=f"mode {mode} position {position}")
+        g2.close()

@@ -69,3 +69,28 @@ def test_static_workspace_largest_and_too_large(gpu):
     z = torch.zeros(16, device="cuda", dtype=torch.bfloat16)
     with pytest.raises(ops.Qwen35PrimitiveError, match="static decode workspace is too small"):
         ops.qwen35_online_attention_decode_static_workspace(z, z, z, z, z, z, shape, 3, 1, 1, plan)
+
+
+def test_static_workspace_under_graph_capture(gpu):
+    # After one eager call on the device, the allocation-free entry point is captured into a
+    # HIP graph (torch.cuda.graph) and replayed; each replay, with eager work and
+    # synchronisations between replays, must give exactly the workspace entry point's output.
+    ctx, max_ctx = 3000, 4096
+    ref_out, _, _, _ = _both(ctx, max_ctx, 45)  # also the eager first call on this device
+    x, cache = _case(ctx, max_ctx, 45)
+    shape = S(1, HQ, HKV, D, max_ctx, ctx - 1)
+    plan = ops.qwen35_online_decode_plan(shape, ops.SPLIT_K_256, max_ctx)
+    pos = torch.tensor([ctx - 1], device="cuda", dtype=torch.int32)
+    out = torch.empty(HQ * D, device="cuda", dtype=torch.bfloat16)
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        ops.qwen35_online_attention_decode_static_workspace(*x, out, cache, shape, 3, 1, 1, plan,
+                                                            device_position=pos,
+                                                            stream=side)
+    for replay in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref_out), f"replay {replay}"
