@@ -325,6 +325,26 @@ def main():
 
     if args.counters:
         split_decode(4096, counters=True)
+        # The ctx 4096 split-K call in its device-position form, 20 times with a
+        # valid position and 20 times with position == max_ctx, where both of
+        # its kernels return right after reading the position: the second set
+        # is the merge kernel's fixed fetch (code, arguments, position) with the
+        # same grid and arguments and no partial read.
+        mshape = ops.Qwen35AttentionShape(1, HQ, HKV, D, 4096, 0)
+        mplan = ops.qwen35_online_decode_plan(mshape, ops.AUTO, 4096)
+        mws = torch.empty(ops.qwen35_online_decode_workspace_layout(mshape, mplan[0])[4],
+                          device="cuda", dtype=torch.uint8)
+        mcache = make_caches(4096, 1)[0]
+        mq, mk, mv, mg = rand_bf16(HQ * D), rand_bf16(HKV * D), rand_bf16(HKV * D), rand_bf16(HQ * D)
+        mout = torch.empty(HQ * D, device="cuda", dtype=torch.bfloat16)
+        for position in (4095, 4096):
+            mpos = torch.tensor([position], device="cuda", dtype=torch.int32)
+            for _ in range(20):
+                ops.qwen35_online_attention_decode(mq, mk, mv, mg, mout, mcache, mws, mshape,
+                                                   ops.DTYPE_BF16, ops.CACHE_BF16, ops.HEAD_MAJOR,
+                                                   plan=mplan, device_position=mpos, stream=stream)
+        torch.cuda.synchronize()
+        del mcache
         src = torch.empty(64 << 20, device="cuda", dtype=torch.uint8)
         dst = torch.empty_like(src)
         src.fill_(1)
@@ -363,7 +383,8 @@ def main():
                                         lg[i:i + 1], 128 ** -0.5, st, o5[:1], None, False,
                                         stream=stream)
         torch.cuda.synchronize()
-        log("counters run: 20 partition launches (ctx 4096), 20 copies of 64 MiB, 20 PP512 "
+        log("counters run: 20 partition launches (ctx 4096), 20 + 20 device-position decode calls "
+            "(valid, then past the maximum context), 20 copies of 64 MiB, 20 PP512 "
             "prefill kernels, 10 delta prefills (T=512), 20 delta decode steps")
         return
 

@@ -92,6 +92,14 @@ std::size_t chunk_record_bytes(std::size_t tokens, std::size_t hv, std::size_t d
                           record, "gated-delta workspace shape overflow");
 }
 
+// The model shapes whose convolution runs channel-spread (conv_norm_wide_kernel):
+// their chunked prefill uses the 33,024-byte T-records, so the workspace is
+// sized for those; other dk = dv = 128 shapes take the 147,712-byte W/U records.
+bool channel_spread_shape(const GatedDeltaShape &s, std::size_t conv_dim) {
+  return s.key_dim == kChunkDim && s.value_dim == kChunkDim && s.conv_width == 4 && conv_dim % 2048 == 0 &&
+         s.hidden_size % 2048 == 0;
+}
+
 struct CheckedShape {
   std::size_t key_size, value_size, conv_dim, token_stride, convolution_elements,
       recurrent_elements, workspace_bytes;
@@ -140,7 +148,9 @@ CheckedShape validate_shape(const GatedDeltaShape &s) {
   std::size_t ws_bytes = checked_mul<Err>(
       checked_mul<Err>(s.tokens, per_token, "gated-delta workspace shape overflow"), sizeof(float),
       "gated-delta workspace byte size overflow");
-  const std::size_t records = chunk_record_bytes(s.tokens, s.value_heads, s.key_dim, s.value_dim);
+  const std::size_t records =
+      chunk_record_bytes(s.tokens, s.value_heads, s.key_dim, s.value_dim,
+                         channel_spread_shape(s, conv_dim) ? rec2::kBytes : rec::kBytes);
   if (records != 0)
     ws_bytes = checked_add<Err>(record_offset(ws_bytes), records,
                                 "gated-delta workspace byte size overflow");
@@ -2497,12 +2507,16 @@ void launch_typed(const DeltaSources &src, const void *conv_weight, const void *
   // The channel-spread convolution also reads weights and history as vectors.
   const bool wide = fast && ((reinterpret_cast<std::uintptr_t>(conv_weight) |
                               reinterpret_cast<std::uintptr_t>(conv_state)) & 15u) == 0;
-  const bool chunked = use_chunked(s, policy) && (reinterpret_cast<std::uintptr_t>(ws) & 15u) == 0;
+  const bool chunk_eligible = use_chunked(s, policy) && (reinterpret_cast<std::uintptr_t>(ws) & 15u) == 0;
   const bool one_token_state = wide && s.tokens == 1;
   // The chunked path on the wide convolution takes q / k / v as (hi, lo)
   // bf16 planes (chunk_tb_kernel<true> + chunk_tscan_split_kernel).
-  const bool split_chunked = wide && chunked && !one_token_state && s.key_dim == kChunkDim &&
+  const bool split_chunked = wide && chunk_eligible && !one_token_state && s.key_dim == kChunkDim &&
                              s.value_dim == kChunkDim;
+  // The W/U-record path needs records of rec::kBytes, which the workspace
+  // holds only for shapes that are not channel-spread; a channel-spread shape
+  // whose pointers rule out the wide convolution runs the recurrent kernels.
+  const bool chunked = chunk_eligible && (split_chunked || !channel_spread_shape(s, c.conv_dim));
   constexpr int kConvTokens = 4; // tokens per workgroup of the multi-token convolution
   // A one-token call of the model shape (two value heads per key head): the
   // convolution, recurrence and output norm in one kernel.

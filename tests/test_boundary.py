@@ -173,6 +173,19 @@ def test_delta_workspace_linear_and_validation():
     one, four = G(1, 28, 2, 4, 5, 7, 3, 1e-6), G(4, 28, 2, 4, 5, 7, 3, 1e-6)
     # cpp/tests/qwen35_cuda_delta_test.cu:785-787
     assert ops.qwen35_gated_delta_workspace_bytes(four) == 4 * ops.qwen35_gated_delta_workspace_bytes(one)
+    # The model shape at T=512: the per-token buffers (conv outputs, raw output, beta and
+    # decay: T (conv_dim + hidden + 2 hv) fp32) plus one 33,024-byte T-record per (value
+    # head, 64-token chunk); the reference's own workspace is T (conv_dim + hidden) fp32
+    # (cpp/kernels/qwen35_delta.cu:757-759), 25,165,824 bytes here.
+    model = G(512, 4096, 16, 32, 128, 128, 4, 1e-6)
+    per_token = 512 * (8192 + 4096 + 64) * 4
+    want = ((per_token + 255) // 256) * 256 + 32 * 8 * 33024
+    assert ops.qwen35_gated_delta_workspace_bytes(model) == want
+    assert want <= 1.4 * 512 * (8192 + 4096) * 4
+    # other dk = dv = 128 shapes keep the W/U records (147,712 bytes each)
+    small = G(512, 512, 2, 4, 128, 128, 4, 1e-6)
+    per_token = 512 * (1024 + 512 + 8) * 4
+    assert ops.qwen35_gated_delta_workspace_bytes(small) == ((per_token + 255) // 256) * 256 + 4 * 8 * 147712
     f = FakeTensor()
     bad_shapes = [G(0, 28, 2, 4, 5, 7, 3, 1e-6), G(1, 29, 2, 4, 5, 7, 3, 1e-6),
                   G(1, 21, 2, 3, 5, 7, 3, 1e-6), G(1, 28, 2, 4, 5, 7, 0, 1e-6),
