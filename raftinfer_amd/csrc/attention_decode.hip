@@ -11,7 +11,9 @@
 #include "norm_rope.hpp"
 #include "raftinfer_amd/qwen35_online_attention.hpp"
 
+#include <algorithm>
 #include <atomic>
+#include <bit>
 #include <type_traits>
 #include <cmath>
 #include <mutex>
@@ -71,29 +73,33 @@ std::size_t ceil_div(std::size_t n, std::size_t d, const char *message) {
   return n / d + (n % d == 0 ? 0 : 1);
 }
 
-// cpp/kernels/qwen35_online_attention.cu:171-183
+// Partition length of a resolved mode (cpp/kernels/qwen35_online_attention.cu:
+// 171-183): the split modes name theirs, the others have none.
 std::size_t partition_tokens_for_mode(Qwen35DecodeAttentionMode mode) {
-  switch (mode) {
-  case Qwen35DecodeAttentionMode::split_k_256: return 256;
-  case Qwen35DecodeAttentionMode::split_k_512: return 512;
-  case Qwen35DecodeAttentionMode::single_block:
-  case Qwen35DecodeAttentionMode::auto_select: return 0;
-  }
-  require<Err>(false, "unsupported online decode attention mode");
+  if (mode == Qwen35DecodeAttentionMode::split_k_256) return 256;
+  if (mode == Qwen35DecodeAttentionMode::split_k_512) return 512;
+  require<Err>(mode == Qwen35DecodeAttentionMode::single_block ||
+                   mode == Qwen35DecodeAttentionMode::auto_select,
+               "unsupported online decode attention mode");
   return 0;
 }
 
-// cpp/kernels/qwen35_online_attention.cu:185-196
+// The context bucket (the plan's context_bucket_tokens, which fixes the
+// partition capacity a captured decode graph is built for): the smallest
+// power of two that is at least 512 and at least the context, capped at the
+// maximum context.  A context beyond the largest power of two a size_t holds
+// gets the maximum context.  The reference reaches the same value by doubling
+// 512 in a loop (cpp/kernels/qwen35_online_attention.cu:185-196); the plan
+// tests compare the two over every boundary.
 std::size_t context_bucket_tokens(Qwen35AttentionShape shape, std::size_t context_tokens) {
+  static_assert(std::has_single_bit(kMinimumContextBucketTokens));
+  constexpr std::size_t kTopPower = std::size_t{1} << (std::numeric_limits<std::size_t>::digits - 1);
   std::size_t bucket = kMinimumContextBucketTokens;
-  while (bucket < context_tokens && bucket < shape.max_context_tokens) {
-    if (bucket > std::numeric_limits<std::size_t>::max() / 2) {
-      bucket = shape.max_context_tokens;
-      break;
-    }
-    bucket *= 2;
-  }
-  return bucket < shape.max_context_tokens ? bucket : shape.max_context_tokens;
+  if (context_tokens > kTopPower)
+    bucket = shape.max_context_tokens;
+  else if (context_tokens > bucket)
+    bucket = std::bit_ceil(context_tokens);
+  return std::min(bucket, shape.max_context_tokens);
 }
 
 int grid_dim(std::size_t value, const char *message) {

@@ -53,6 +53,18 @@ def test_decode_plan_bit_exact_with_oracle(max_ctx, mode):
                        want.context_bucket_tokens, want.active_partition_capacity)
 
 
+def test_decode_plan_bucket_at_the_size_limit():
+    # The bucket's overflow guard (cpp/kernels/qwen35_online_attention.cu:188-191): contexts
+    # next to and past the largest power of two a size_t holds, single-block plans.
+    top = 2 ** 64 - 1
+    for ctx in (2 ** 62 + 1, 2 ** 63 - 1, 2 ** 63, 2 ** 63 + 1, top - 1, top):
+        for max_ctx in (ctx, top):
+            want = orc.decode_plan((1, 16, 4, 256, max_ctx), 1, ctx)
+            got = ops.qwen35_online_decode_plan(S(1, 16, 4, 256, max_ctx, 0), 1, ctx)
+            assert got == (want.resolved_mode, want.partition_tokens, want.split_k_threshold_tokens,
+                           want.context_bucket_tokens, want.active_partition_capacity), (ctx, max_ctx)
+
+
 @pytest.mark.parametrize("shape", [(1, 16, 4, 256, 4096), (1, 16, 4, 256, 1025), (1, 16, 4, 256, 1),
                                    (1, 16, 4, 255, 4096), (2, 16, 4, 256, 64), (1, 8, 4, 256, 64)])
 def test_workspace_layout_bit_exact_with_oracle(shape):
