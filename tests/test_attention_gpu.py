@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import (HKV, HQ, D, assert_bf16_close, bf16, cache_index, close_enough, from_dev,
+from helpers import (HKV, HQ, D, assert_bf16_close, bf16, close_enough, from_dev,
                      make_cache, normal, read_cache, rng, to_dev)
 from oracle import pyoracle as orc
 from raftinfer_amd import ops

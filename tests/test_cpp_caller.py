@@ -9,7 +9,7 @@ import subprocess
 import numpy as np
 import pytest
 
-from helpers import HKV, HQ, D, assert_bf16_close, bf16, close_enough, rel_l2
+from helpers import HKV, HQ, D, assert_bf16_close, close_enough, rel_l2
 from oracle import pyoracle as orc
 
 HERE = pathlib.Path(__file__).resolve().parent
