@@ -361,3 +361,37 @@ def test_unpacked_entry_validation(gpu):
     with pytest.raises(ops.Qwen35DeltaError, match="alpha is not dtype-aligned"):
         # f32 activations need 4-byte alignment; one bf16 element in is 2-byte aligned
         ops.qwen35_gated_delta_unpacked(z, z, z[1:], z, z, z, z, z, z, st, st, ws, shape, 1, 1)
+
+
+def test_channel_spread_shape_off_the_wide_path_stays_in_its_workspace(gpu):
+    # A model-shape prefill long enough to be chunked (T = 128) whose packed input is not
+    # 16-byte aligned, so the channel-spread convolution cannot run.  The workspace of this
+    # shape holds T-records only (33,024 B each), so the call must take the recurrent kernels
+    # rather than the W/U-record path: checked against the oracle, with a guard region after
+    # the workspace that must come back untouched.
+    sh = model_shape(128)
+    fx = fixture_for(sh, seed=1280)
+    r = rng(1281)
+    cd = 2 * sh["hk"] * 128 + sh["hv"] * 128
+    conv0 = normal(r, cd * 3)
+    rec0 = normal(r, sh["hv"] * 128 * 128, scale=0.05)
+    shape = ops.GatedDeltaShape(128, sh["hidden"], sh["hk"], sh["hv"], 128, 128, 4, sh["eps"])
+    need = ops.qwen35_gated_delta_workspace_bytes(shape)
+    guard = 1 << 16
+    buf = torch.full((need + guard,), 0x5A, device="cuda", dtype=torch.uint8)
+    ws = buf[:need]
+    inp = to_dev(fx["inp"], torch.bfloat16)
+    shifted = torch.empty(inp.numel() + 1, device="cuda", dtype=torch.bfloat16)
+    shifted[1:].copy_(inp)
+    conv = to_dev(conv0, torch.float32)
+    rec = to_dev(rec0, torch.float32)
+    out = torch.empty(128 * sh["hidden"], device="cuda", dtype=torch.bfloat16)
+    w = {k: to_dev(fx[k], torch.bfloat16) for k in ("cw", "a", "dt", "nw")}
+    ops.qwen35_gated_delta(shifted[1:], w["cw"], w["a"], w["dt"], w["nw"], out, conv, rec, ws, shape, 3, 3)
+    torch.cuda.synchronize()
+    assert bool((buf[need:] == 0x5A).all()), "the call wrote past its workspace"
+    want = run_ref(sh, fx, 3, 3, conv0, rec0)
+    got = (from_dev(out), from_dev(conv), from_dev(rec))
+    check(got, want)
+    assert rel_l2(got[2], want[2]) < 1e-4
+    assert_bf16_close(got[0], want[0], what="off-wide T=128")
