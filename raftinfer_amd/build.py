@@ -43,12 +43,39 @@ def _compile(src: pathlib.Path) -> pathlib.Path:
     return obj
 
 
+# Sources whose kernels issue MFMAs from inline asm; their gfx950 assembly is
+# checked for reads of an MFMA result inside its latency (asm_check.py).
+ASM_CHECKED = ("attention_prefill_mfma.hip",)
+
+
+def _check_asm(name: str) -> None:
+    try:
+        from .asm_check import asm_mfma_hazards
+    except ImportError:  # run as a script
+        sys.path.insert(0, str(PKG))
+        from asm_check import asm_mfma_hazards
+
+    src = CSRC / name
+    out = BUILD / (name + ".s")
+    cmd = [HIPCC, *FLAGS, "-x", "hip", "--cuda-device-only", "-S", str(src), "-o", str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed for {name}:\n{res.stderr}")
+    hazards = asm_mfma_hazards(out.read_text())
+    if hazards:
+        raise RuntimeError(f"{name}: inline-asm MFMA results read too early "
+                           f"({len(hazards)}):\n" + "\n".join(hazards[:10]))
+
+
 def build(jobs: int | None = None) -> pathlib.Path:
     BUILD.mkdir(exist_ok=True)
     sources = sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
-    jobs = jobs or min(8, len(sources))
+    jobs = jobs or min(8, len(sources) + len(ASM_CHECKED))
     with cf.ThreadPoolExecutor(jobs) as pool:
+        checks = [pool.submit(_check_asm, name) for name in ASM_CHECKED]
         objs = list(pool.map(_compile, sources))
+        for c in checks:
+            c.result()
     tmp = LIB.with_suffix(".so.tmp")
     subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
                     *map(str, objs)], check=True)

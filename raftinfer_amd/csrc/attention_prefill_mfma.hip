@@ -115,7 +115,11 @@ __host__ __device__ constexpr std::size_t ceil_div_u(std::size_t n, std::size_t 
 // The compiler would otherwise move all 128 accumulator registers between
 // AGPRs and VGPRs around every tile because of the (rare) rescale code.  The
 // s_nop covers the VALU-write -> MFMA-read hazard of the operands, which the
-// hazard recognizer does not see through asm.
+// hazard recognizer does not see through asm.  For the same reason the
+// compiler does not know the MFMA's result latency: a register copy of `o`
+// placed right after this statement would read it before it is written.  The
+// build (raftinfer_amd/asm_check.py) scans this file's assembly and fails on
+// any such read; the drain below covers the reads the kernel itself makes.
 __device__ __forceinline__ void mfma_acc_agpr(floatx16 &o, bf16x8 a, bf16x8 b) {
   asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(o) : "v"(a), "v"(b));
 }
