@@ -444,7 +444,12 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(
     }
     mx = max_xor32(mx);
     const bool grow = mx > m_run + kLazyRescale;
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+    if (first) {
+      // A wave's first tile: nothing is accumulated yet (m = -inf, l = 0,
+      // o = 0), so the new max needs no rescale of the accumulators (the
+      // rescale moves all 128 of them through VGPRs; PP128 7.24 -> 6.86 us).
+      m_run = grow ? mx : m_run;
+    } else if (__builtin_amdgcn_ballot_w64(grow) != 0) {
       // Lanes that do not grow keep their scale (1, also when m is still -inf).
       const float m_new = grow ? mx : m_run;
       const float sc = grow ? fexp2(m_run - mx) : 1.0f; // -inf -> 0 on a first tile
