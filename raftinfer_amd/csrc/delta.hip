@@ -206,8 +206,11 @@ __device__ __forceinline__ void split2(float a, float b, std::uint32_t &h, std::
   h = pack_bf16x2(a, b);
   l = pack_bf16x2(a - bf16_lo(h), b - bf16_hi(h));
 }
-__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
-__device__ __forceinline__ float sigmoid(float v) { return 1.0f / (1.0f + __expf(-v)); }
+// The hardware reciprocal (1 ulp) instead of an IEEE division, whose
+// scale / FMA / fix-up sequence per element made SiLU the costliest part of
+// the convolution and output norm (T = 512 entry 45.5 -> 44.4 us).
+__device__ __forceinline__ float silu(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
+__device__ __forceinline__ float sigmoid(float v) { return __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
 __device__ __forceinline__ float softplus(float v) {
   if (v > 20.0f) return v;
   if (v < -20.0f) return __expf(v);
