@@ -38,9 +38,12 @@ def _agprs(operand: str):
 def asm_mfma_hazards(assembly: str) -> list[str]:
     """Reads of an inline-asm MFMA's destination AGPRs issued fewer than
     RESULT_WAIT_STATES wait states after it (s_nop n counts n + 1, any other
-    instruction 1; code is followed in listing order, labels included, so a
-    fall-through is checked like straight-line code).  MFMA -> MFMA
-    accumulator chains are left to the hardware's dependency check."""
+    instruction 1).  Code is followed in listing order, labels included, so a
+    fall-through is checked like straight-line code; a taken branch is not
+    followed (the kernel drains its asm MFMAs before each loop back-edge).
+    Reads by other MFMAs are not checked: the kernel's accumulators feed only
+    the next MFMA of their own chain, which the hardware's dependency check
+    covers."""
     hazards: list[str] = []
     pending: list[list[int]] = []  # [first AGPR, last AGPR, wait states left, line]
     in_asm = False
